@@ -1,0 +1,155 @@
+"""ctypes binding of ``libfa_hip.so``: public inputs q/k/v, public output O.
+
+Mirrors the reference's operator binding
+(``backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/binding.py:6-110``):
+
+  * the library is opened with ``RTLD_LOCAL``;
+  * a call is two-phase: ``fa_fwd_workspace_bytes`` sizes the workspace,
+    ``fa_fwd`` enqueues the forward on the current torch stream;
+  * geometry, dtype, device and layout errors raise ``ValueError`` before any
+    launch; a nonzero library status raises ``RuntimeError("fa_fwd <where>:
+    <status> (<message>)")``;
+  * output and workspace tensors are allocated by torch, cached per
+    (shapes, device, config), and the same cached output tensor is returned
+    on every call; the workspace grows on demand.
+
+Nothing here falls back to another implementation: without the built library
+construction fails.
+"""
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+
+FA_ACC = {"fp32": 0, "fp16": 1}
+
+
+class FaProblem(C.Structure):
+    _fields_ = [
+        ("batch", C.c_int64),
+        ("heads_q", C.c_int64),
+        ("heads_kv", C.c_int64),
+        ("seq_q", C.c_int64),
+        ("seq_k", C.c_int64),
+        ("dim", C.c_int64),
+        ("scale", C.c_float),
+        ("acc", C.c_int32),
+        ("kernel", C.c_int32),
+        ("reserved", C.c_int32),
+    ]
+
+
+# Every symbol include/fa_hip.h declares, with its ctypes signature.
+SIGNATURES = {
+    "fa_fwd_workspace_bytes": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_uint64)]),
+    "fa_fwd": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                         C.c_void_p, C.c_uint64, C.c_void_p]),
+    "fa_fwd_tile": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
+    "fa_kernel_count": (C.c_int, []),
+    "fa_kernel_name": (C.c_char_p, [C.c_int32]),
+    "fa_strerror": (C.c_char_p, [C.c_int]),
+}
+
+
+def load_library(path):
+    """Open the shared library and attach the C signatures of every entry point."""
+    lib = C.CDLL(str(path), mode=C.RTLD_LOCAL)
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return lib
+
+
+@dataclass(frozen=True)
+class AttentionConfig:
+    """Launch configuration: accumulation variant and tile selector (0 = automatic)."""
+    acc: str = "fp32"
+    kernel: int = 0
+
+    def __post_init__(self):
+        if self.acc not in FA_ACC:
+            raise ValueError(f"unknown accumulation variant {self.acc!r}")
+        if not isinstance(self.kernel, int) or self.kernel < 0:
+            raise ValueError("kernel selector must be a non-negative int")
+
+
+def make_problem(q_shape, k_shape, scale, config):
+    b, hq, nq, d = q_shape
+    _, hkv, nk, _ = k_shape
+    return FaProblem(b, hq, hkv, nq, nk, d, float(scale), FA_ACC[config.acc], config.kernel, 0)
+
+
+class Operator:
+    """Callable ``(q, k, v) -> o`` over ``libfa_hip.so``."""
+
+    def __init__(self, library, config=AttentionConfig()):
+        self.config = config
+        self.lib = load_library(library) if not isinstance(library, C.CDLL) else library
+        self.workspace = None
+        self.buffers = {}
+
+    def message(self, status):
+        text = self.lib.fa_strerror(status)
+        return text.decode() if text else "unknown status"
+
+    def check(self, status, where):
+        if status:
+            raise RuntimeError(f"fa_fwd {where}: {status} ({self.message(status)})")
+
+    def tile(self, q_shape, k_shape):
+        """(query rows, keys) granularity of the kernel the library would use."""
+        prob = make_problem(q_shape, k_shape, 1.0, self.config)
+        rows, keys = C.c_int32(), C.c_int32()
+        self.check(self.lib.fa_fwd_tile(C.byref(prob), C.byref(rows), C.byref(keys)), "tile")
+        return rows.value, keys.value
+
+    def validate(self, q, k, v):
+        import torch
+
+        if q.ndim != 4 or k.ndim != 4 or v.shape != k.shape:
+            raise ValueError("Q/K/V must be [B,H,N,128]")
+        b, h, nq, d = q.shape
+        if min(q.shape) <= 0 or min(k.shape) <= 0 or k.shape[0] != b or d != 128 \
+                or k.shape[3] != 128 or h % k.shape[1]:
+            raise ValueError("invalid attention geometry")
+        rows, keys = self.tile(q.shape, k.shape)
+        if nq % rows or k.shape[2] % keys or max(nq, k.shape[2]) >= 2 ** 30:
+            raise ValueError(f"unsupported query/key tail (Nq % {rows}, Nk % {keys})")
+        for t in (q, k, v):
+            if t.device.type != "cuda" or t.device != q.device or t.dtype != torch.float16 \
+                    or not t.is_contiguous():
+                raise ValueError("Q/K/V must be contiguous FP16 on the same GPU")
+
+    def buffers_for(self, q, k):
+        import torch
+
+        key = (tuple(q.shape), tuple(k.shape), q.device, self.config)
+        if key not in self.buffers:
+            self.buffers[key] = torch.empty(q.shape, dtype=torch.float16, device=q.device)
+        return self.buffers[key]
+
+    def __call__(self, q, k, v, scale=None):
+        import torch
+
+        self.validate(q, k, v)
+        scale = q.shape[3] ** -0.5 if scale is None else float(scale)
+        if not (scale > 0 and math.isfinite(scale)):
+            raise ValueError("scale must be finite and positive")
+        prob = make_problem(q.shape, k.shape, scale, self.config)
+        size = C.c_uint64()
+        self.check(self.lib.fa_fwd_workspace_bytes(C.byref(prob), C.byref(size)), "prepare")
+        out = self.buffers_for(q, k)
+        with torch.cuda.device(q.device):
+            need = max(size.value, 16)
+            if self.workspace is None or self.workspace.device != q.device \
+                    or self.workspace.numel() < need:
+                self.workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+            stream = torch.cuda.current_stream(q.device)
+            self.check(self.lib.fa_fwd(C.byref(prob), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                       out.data_ptr(), self.workspace.data_ptr(),
+                                       self.workspace.numel(), C.c_void_p(stream.cuda_stream)),
+                       "launch")
+            for t in (q, k, v, out, self.workspace):
+                t.record_stream(stream)
+        return out

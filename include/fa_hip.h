@@ -1,0 +1,103 @@
+/*
+ * fa_hip.h -- C ABI of libfa_hip.so, the MI355X (gfx950) flash-attention
+ * forward for non-causal grouped-query attention, FP16 in and FP16 out.
+ *
+ * Layout: q [B, Hq, Nq, 128], k and v [B, Hkv, Nk, 128], o [B, Hq, Nq, 128],
+ * all contiguous FP16 in device memory. Output rows are the normalised
+ * softmax(q k^T * scale) v with query head h reading key/value head
+ * h / (Hq / Hkv).
+ *
+ * Conventions (mirroring the reference's two-phase operator binding):
+ *   - every entry point returns 0 on success and a nonzero FA_ERR_* code
+ *     otherwise; fa_strerror() names the code;
+ *   - nothing here allocates device memory, aborts, or keeps mutable global
+ *     state: the caller owns q, k, v, o and the workspace, and calls on
+ *     different streams are independent;
+ *   - fa_fwd() is asynchronous on the given stream (a hipStream_t passed as
+ *     void*, NULL for the default stream).
+ *
+ * This header needs no HIP or torch headers, so any FFI (ctypes, cgo, JNI)
+ * can bind it directly.
+ */
+#ifndef FA_HIP_H
+#define FA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum fa_status {
+  FA_OK = 0,
+  FA_ERR_NULL = 1,          /* a required pointer is NULL */
+  FA_ERR_GEOMETRY = 2,      /* non-positive size, Hq % Hkv != 0, or overflowing sizes */
+  FA_ERR_DIM = 3,           /* head dimension other than 128 */
+  FA_ERR_TAIL = 4,          /* Nq or Nk not a multiple of the selected tile */
+  FA_ERR_ALIGN = 5,         /* a tensor pointer is not 16-byte aligned */
+  FA_ERR_WORKSPACE = 6,     /* workspace missing or smaller than fa_fwd_workspace_bytes() */
+  FA_ERR_ACC = 7,           /* unknown accumulation variant */
+  FA_ERR_SCALE = 8,         /* scale not finite and positive */
+  FA_ERR_KERNEL = 9,        /* unknown kernel selector */
+  FA_ERR_LAUNCH = 10        /* the HIP runtime rejected a launch */
+};
+
+enum fa_acc {
+  FA_ACC_FP32 = 0,          /* O accumulated in FP32 registers across all keys */
+  FA_ACC_FP16 = 1           /* per-block PV rounded to FP16, O accumulated in FP16 */
+};
+
+typedef struct fa_problem {
+  int64_t batch;            /* B */
+  int64_t heads_q;          /* Hq */
+  int64_t heads_kv;         /* Hkv, divides Hq */
+  int64_t seq_q;            /* Nq */
+  int64_t seq_k;            /* Nk */
+  int64_t dim;              /* D, must be 128 */
+  float scale;              /* softmax scale, normally dim ** -0.5 */
+  int32_t acc;              /* enum fa_acc */
+  int32_t kernel;           /* 0 = automatic tile choice; k >= 1 forces tile configuration k */
+  int32_t reserved;         /* must be 0 */
+} fa_problem;
+
+/*
+ * Bytes of device workspace fa_fwd() needs for problem *p (the key-permuted
+ * transposed copy of v). Replaces phase 1 of the reference's operator call,
+ * aclnn<Op>GetWorkspaceSize (backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/
+ * binding.py:21-24,74-75), whose host tiling sizes the scratch buffer
+ * (project/op_host/fa_fa_nk_nz_vector_fp32_v5_sumpack.cpp:52-87).
+ */
+int fa_fwd_workspace_bytes(const fa_problem* p, uint64_t* bytes);
+
+/*
+ * Enqueue one attention forward on `stream`: o = softmax(q k^T * scale) v.
+ * Replaces phase 2 of the reference's operator call, aclnn<Op>(workspace,
+ * size, executor, stream) (backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/
+ * binding.py:25-27,80), and the external reference op it is checked against
+ * (backends/npu_fa/backend.py:36-49). The workspace must hold at least
+ * fa_fwd_workspace_bytes(p) bytes; its contents on entry do not matter.
+ */
+int fa_fwd(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
+           void* workspace, uint64_t workspace_bytes, void* stream);
+
+/*
+ * Query-row and key-block granularity of the kernel fa_fwd() would use for
+ * *p: Nq must be a multiple of *rows and Nk of *keys. Host-side counterpart
+ * of the reference binding's alignment check (binding.py:95).
+ */
+int fa_fwd_tile(const fa_problem* p, int32_t* rows, int32_t* keys);
+
+/* Number of selectable tile configurations (valid fa_problem.kernel values are 1..n). */
+int fa_kernel_count(void);
+
+/* Static name of tile configuration `kernel` (1..fa_kernel_count()), or NULL. */
+const char* fa_kernel_name(int32_t kernel);
+
+/* Static message for a status code. */
+const char* fa_strerror(int status);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_HIP_H */

@@ -1,0 +1,187 @@
+"""CPU oracle for the attention forward -- TEST INFRASTRUCTURE, NOT PRODUCT CODE.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import this module, and only as the checker or as the
+timed CPU baseline; the shipped path (``fa_amd``) never imports it and has no
+CPU fallback.
+
+What it restates (the reference's algorithm for this path):
+  * the op semantics of the reference backend ``npu_fa``
+    (``backends/npu_fa/backend.py:36-49``): BNSD layout, non-causal, no mask,
+    no dropout, ``scale = dim ** -0.5``, native GQA with query head ``h``
+    reading key/value head ``h // (Hq / Hkv)``;
+  * the canonical formula ``ref_flash_attn``
+    (``backends/expert_v2/impl.py:701-716``): repeat K/V per query group,
+    ``softmax(q k^T * scale) v`` computed in FP32, output rounded to FP16;
+  * the check of ``core/runner.py:57-72`` / ``core/bench.py:131-144``:
+    compare ``out.float()`` with ``ref.float()`` and report ``max|diff|``.
+
+Functions and what pins each (tests/test_oracle.py):
+  attention_loops      pure-Python definition for tiny shapes; pinned by
+                       hand-computed closed forms (single key, equal logits).
+  attention_f64        float64 numpy; pinned against attention_loops, against
+                       torch's scaled_dot_product_attention in float64 (the
+                       library routine the reference's formula calls), and by
+                       closed forms (constant V, identical keys, one dominant
+                       key, Nk = 1) and invariants (joint K/V permutation,
+                       q shifted orthogonally to every key, GQA == repeated
+                       MHA, scale folded into q).
+  attention_rows_f64   rows of attention_f64 for sampled (b, h, i); pinned by
+                       equality with the full computation (rows are independent).
+  attention_f32        the canonical FP32 formula on CPU torch, chunked; pinned
+                       against attention_f64 (FP32 rounding bound) and torch's
+                       float32 scaled_dot_product_attention. It is also the
+                       CPU baseline bench.py times.
+Every check above plants a mistake in the oracle (dropped scale, swapped GQA
+map, transposed operand) and confirms at least one check fails
+(tests/test_oracle.py::test_checks_catch_planted_mistakes).
+"""
+
+import numpy as np
+
+
+def _np(x):
+    """numpy view of a torch tensor or array-like (CPU)."""
+    if hasattr(x, "detach"):
+        x = x.detach().cpu().numpy()
+    return np.asarray(x)
+
+
+def _scale(d, scale):
+    return float(d) ** -0.5 if scale is None else float(scale)
+
+
+def attention_loops(q, k, v, scale=None):
+    """Definition by loops: o[b,h,i] = sum_j softmax_j(q.k_j * scale) v_j.
+
+    Intended for tiny shapes only (pure Python).
+    """
+    import math
+
+    q, k, v = (_np(t).astype(np.float64) for t in (q, k, v))
+    b_, hq, nq, d = q.shape
+    hkv, nk = k.shape[1], k.shape[2]
+    group = hq // hkv
+    sc = _scale(d, scale)
+    out = np.zeros((b_, hq, nq, d))
+    for b in range(b_):
+        for h in range(hq):
+            hk = h // group
+            for i in range(nq):
+                logits = []
+                for j in range(nk):
+                    dot = 0.0
+                    for x in range(d):
+                        dot += q[b, h, i, x] * k[b, hk, j, x]
+                    logits.append(dot * sc)
+                mx = max(logits)
+                w = [math.exp(t - mx) for t in logits]
+                z = sum(w)
+                for x in range(d):
+                    acc = 0.0
+                    for j in range(nk):
+                        acc += w[j] * v[b, hk, j, x]
+                    out[b, h, i, x] = acc / z
+    return out
+
+
+def _softmax_rows_f64(s):
+    s = s - s.max(axis=-1, keepdims=True)
+    np.exp(s, out=s)
+    s /= s.sum(axis=-1, keepdims=True)
+    return s
+
+
+def attention_f64(q, k, v, scale=None, chunk_rows=1024):
+    """Exact-as-float64 attention over [B,H,N,D]; returns float64 [B,Hq,Nq,D]."""
+    q, k, v = (_np(t) for t in (q, k, v))
+    b_, hq, nq, d = q.shape
+    hkv, nk = k.shape[1], k.shape[2]
+    if hq % hkv:
+        raise ValueError("heads_q must be a multiple of heads_kv")
+    group = hq // hkv
+    sc = _scale(d, scale)
+    out = np.empty((b_, hq, nq, d), dtype=np.float64)
+    for b in range(b_):
+        for h in range(hq):
+            kf = k[b, h // group].astype(np.float64)
+            vf = v[b, h // group].astype(np.float64)
+            for r0 in range(0, nq, chunk_rows):
+                qf = q[b, h, r0:r0 + chunk_rows].astype(np.float64)
+                p = _softmax_rows_f64((qf @ kf.T) * sc)
+                out[b, h, r0:r0 + chunk_rows] = p @ vf
+    return out
+
+
+def attention_rows_f64(q, k, v, rows, scale=None):
+    """float64 output rows for ``rows = [(b, h, i), ...]``; returns [len(rows), D].
+
+    Every output row depends only on its own query row and the full K/V of
+    its key/value head, so sampled rows of an N = 131072 problem are exact
+    references for the corresponding rows of a full GPU result.
+    """
+    q, k, v = (_np(t) for t in (q, k, v))
+    hq, d = q.shape[1], q.shape[3]
+    group = hq // k.shape[1]
+    sc = _scale(d, scale)
+    out = np.empty((len(rows), d), dtype=np.float64)
+    by_head = {}
+    for n, (b, h, i) in enumerate(rows):
+        by_head.setdefault((b, h // group), []).append((n, h, i))
+    for (b, hk), items in by_head.items():
+        kf = k[b, hk].astype(np.float64)
+        vf = v[b, hk].astype(np.float64)
+        qf = np.stack([q[b, h, i].astype(np.float64) for _, h, i in items])
+        p = _softmax_rows_f64((qf @ kf.T) * sc)
+        res = p @ vf
+        for m, (n, _, _) in enumerate(items):
+            out[n] = res[m]
+    return out
+
+
+def attention_f32(q, k, v, scale=None, chunk_elems=1 << 26):
+    """The canonical FP32 formula on CPU torch: FP16 [B,Hq,Nq,D] result.
+
+    K/V heads are repeated per query group implicitly (query head h reads
+    key/value head h // group), scores and softmax run in float32, and the
+    output is rounded to FP16, as in the reference's ``ref_flash_attn``.
+    """
+    import torch
+
+    q, k, v = (t if isinstance(t, torch.Tensor) else torch.from_numpy(np.asarray(t))
+               for t in (q, k, v))
+    b_, hq, nq, d = q.shape
+    hkv, nk = k.shape[1], k.shape[2]
+    group = hq // hkv
+    sc = _scale(d, scale)
+    out = torch.empty((b_, hq, nq, d), dtype=torch.float16)
+    rows = max(1, min(group * nq, chunk_elems // max(nk, 1)))
+    for b in range(b_):
+        for hk in range(hkv):
+            kf = k[b, hk].float()
+            vf = v[b, hk].float()
+            qg = q[b, hk * group:(hk + 1) * group].reshape(group * nq, d)
+            og = out[b, hk * group:(hk + 1) * group].view(group * nq, d)
+            for r0 in range(0, group * nq, rows):
+                s = torch.matmul(qg[r0:r0 + rows].float(), kf.t()) * sc
+                og[r0:r0 + rows] = torch.matmul(torch.softmax(s, dim=-1), vf).to(torch.float16)
+    return out
+
+
+def sample_rows(shape, count, seed=1234):
+    """``count`` distinct (b, h, i) triples spread over a [B,H,N,D] output.
+
+    Always includes the first and last row of the tensor so both ends of the
+    query range are covered.
+    """
+    b_, h_, n_, _ = shape
+    total = b_ * h_ * n_
+    rng = np.random.default_rng(seed)
+    flat = rng.choice(total, size=min(count, total), replace=False)
+    flat = np.unique(np.concatenate([flat, [0, total - 1]]))
+    return [(int(f // (h_ * n_)), int((f // n_) % h_), int(f % n_)) for f in flat]
+
+
+def max_abs_diff(out, ref):
+    """``max |out - ref|`` in float64, the reference harness's reported statistic."""
+    return float(np.max(np.abs(_np(out).astype(np.float64) - _np(ref).astype(np.float64))))

@@ -1,0 +1,112 @@
+"""The C-ABI library loads, exports every declared symbol, and validates on the host.
+
+No compute call runs here: every call below returns an error code before the
+library touches the HIP runtime, so the suite runs without a GPU.
+"""
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from fa_amd import binding
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "fa_hip.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(fa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_binding_signatures():
+    assert declared_functions() == sorted(binding.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(library_path):
+    lib = C.CDLL(library_path, mode=C.RTLD_LOCAL)
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    binding.load_library(library_path)
+
+
+def problem(**kw):
+    base = dict(batch=1, heads_q=12, heads_kv=1, seq_q=4096, seq_k=4096, dim=128,
+                scale=128 ** -0.5, acc=0, kernel=0, reserved=0)
+    base.update(kw)
+    return binding.FaProblem(**base)
+
+
+def ws_bytes(lib, prob):
+    size = C.c_uint64(0)
+    rc = lib.fa_fwd_workspace_bytes(C.byref(prob), C.byref(size))
+    return rc, size.value
+
+
+@pytest.fixture(scope="module")
+def lib(library_path):
+    return binding.load_library(library_path)
+
+
+def test_workspace_size(lib):
+    rc, size = ws_bytes(lib, problem(batch=2, heads_kv=1, seq_k=131072))
+    assert rc == 0 and size == 2 * 1 * 131072 * 128 * 2
+    rc, size = ws_bytes(lib, problem(heads_q=8, heads_kv=4, seq_q=512, seq_k=1024))
+    assert rc == 0 and size == 4 * 1024 * 128 * 2
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(batch=0), 2), (dict(heads_q=12, heads_kv=5), 2), (dict(seq_k=-64), 2),
+    (dict(dim=64), 3), (dict(seq_q=4000), 4), (dict(seq_k=4100), 4),
+    (dict(acc=2), 7), (dict(scale=0.0), 8), (dict(scale=float("inf")), 8),
+    (dict(kernel=99), 9), (dict(reserved=1), 9), (dict(seq_q=1 << 30), 2),
+])
+def test_geometry_errors(lib, kw, code):
+    rc, _ = ws_bytes(lib, problem(**kw))
+    assert rc == code
+    assert lib.fa_strerror(rc)
+
+
+def test_fwd_rejects_before_launch(lib):
+    prob = problem()
+    # NULL tensors, missing workspace and misaligned pointers fail on the host.
+    assert lib.fa_fwd(C.byref(prob), None, None, None, None, None, 0, None) == 1
+    p = C.c_void_p(4096)
+    assert lib.fa_fwd(C.byref(prob), p, p, p, p, None, 0, None) == 6
+    _, size = ws_bytes(lib, prob)
+    assert lib.fa_fwd(C.byref(prob), p, p, p, p, p, size - 1, None) == 6
+    odd = C.c_void_p(4096 + 8)
+    assert lib.fa_fwd(C.byref(prob), p, odd, p, p, p, size, None) == 5
+    assert lib.fa_fwd(None, p, p, p, p, p, size, None) == 1
+
+
+def test_kernel_table(lib):
+    n = lib.fa_kernel_count()
+    assert n >= 1
+    names = [lib.fa_kernel_name(i).decode() for i in range(1, n + 1)]
+    assert len(set(names)) == n
+    assert lib.fa_kernel_name(0) is None and lib.fa_kernel_name(n + 1) is None
+    for i in range(0, n + 1):
+        rows, keys = C.c_int32(), C.c_int32()
+        assert lib.fa_fwd_tile(C.byref(problem(kernel=i)), C.byref(rows), C.byref(keys)) == 0
+        assert rows.value % 32 == 0 and keys.value % 32 == 0
+
+
+def test_operator_validation_without_gpu(library_path):
+    import torch
+
+    op = binding.Operator(library_path)
+    q = torch.zeros(1, 12, 256, 128, dtype=torch.float16)
+    k = torch.zeros(1, 1, 256, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU"):
+        op(q, k, k)
+    with pytest.raises(ValueError, match="geometry"):
+        op(q, torch.zeros(1, 5, 256, 128, dtype=torch.float16),
+           torch.zeros(1, 5, 256, 128, dtype=torch.float16))
+    with pytest.raises(ValueError, match=r"\[B,H,N,128\]"):
+        op(q[0], k, k)
+    with pytest.raises(ValueError, match="tail"):
+        op(q[:, :, :200], k, k)
+    with pytest.raises(ValueError):
+        binding.AttentionConfig(acc="bf16")

@@ -1,0 +1,170 @@
+"""Pins the CPU oracle (oracle/attention.py) without trusting its own formula.
+
+Checks: a pure-loop definition, torch's float64 scaled_dot_product_attention
+(the library routine the reference's canonical formula calls), closed forms,
+invariants, the sampled-row restriction, the FP32 chunked formula, and a test
+that plants mistakes in copies of the oracle to show the checks catch them.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as orc
+
+
+def rand_qkv(b, hq, hkv, nq, nk, d, seed=0, sigma=1.0):
+    rng = np.random.default_rng(seed)
+    q = (rng.standard_normal((b, hq, nq, d)) * sigma).astype(np.float16)
+    k = (rng.standard_normal((b, hkv, nk, d)) * sigma).astype(np.float16)
+    v = rng.standard_normal((b, hkv, nk, d)).astype(np.float16)
+    return q, k, v
+
+
+def sdpa_f64(q, k, v, scale=None):
+    """torch float64 SDPA with K/V repeated per query group."""
+    qt, kt, vt = (torch.from_numpy(np.asarray(t, dtype=np.float64)) for t in (q, k, v))
+    g = qt.shape[1] // kt.shape[1]
+    kt = kt.repeat_interleave(g, dim=1)
+    vt = vt.repeat_interleave(g, dim=1)
+    return torch.nn.functional.scaled_dot_product_attention(
+        qt, kt, vt, attn_mask=None, dropout_p=0.0, is_causal=False, scale=scale).numpy()
+
+
+def test_loops_closed_forms():
+    # One key: the output is that key's value row, whatever the logits.
+    q, k, v = rand_qkv(1, 2, 1, 3, 1, 4)
+    out = orc.attention_loops(q, k, v)
+    np.testing.assert_allclose(out, np.broadcast_to(v.astype(np.float64)[:, :1], out.shape))
+    # Zero query: equal logits, the output is the mean of the value rows.
+    q = np.zeros((1, 1, 2, 4), np.float16)
+    _, k, v = rand_qkv(1, 1, 1, 2, 5, 4)
+    out = orc.attention_loops(q, k, v)
+    np.testing.assert_allclose(out[0, 0, 0], v[0, 0].astype(np.float64).mean(0), rtol=1e-12)
+    # Two keys, hand-computed: logits a, b -> weights e^a/(e^a+e^b).
+    q = np.array([[[[2.0, 0.0]]]], np.float16)
+    k = np.array([[[[1.0, 0.0], [0.0, 1.0]]]], np.float16)
+    v = np.array([[[[1.0, 0.0], [0.0, 1.0]]]], np.float16)
+    out = orc.attention_loops(q, k, v, scale=1.0)
+    w = np.exp(2.0) / (np.exp(2.0) + 1.0)
+    np.testing.assert_allclose(out[0, 0, 0], [w, 1 - w], rtol=1e-12)
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 1, 5, 7, 8), (2, 4, 2, 3, 6, 4), (1, 3, 3, 4, 4, 16)])
+def test_f64_matches_loops(shape):
+    q, k, v = rand_qkv(*shape, seed=3)
+    np.testing.assert_allclose(orc.attention_f64(q, k, v), orc.attention_loops(q, k, v),
+                               rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("shape,sigma", [((1, 12, 1, 64, 96, 128), 1.0),
+                                         ((2, 4, 2, 32, 64, 128), 3.0),
+                                         ((1, 8, 8, 16, 40, 64), 1.0)])
+def test_f64_matches_torch_sdpa(shape, sigma):
+    q, k, v = rand_qkv(*shape, seed=5, sigma=sigma)
+    np.testing.assert_allclose(orc.attention_f64(q, k, v), sdpa_f64(q, k, v),
+                               rtol=1e-9, atol=1e-11)
+
+
+def test_f64_closed_forms():
+    q, k, v = rand_qkv(1, 12, 1, 64, 128, 128, seed=7)
+    # Constant value rows: output equals the constant.
+    vc = np.full_like(v, 0.375)
+    np.testing.assert_allclose(orc.attention_f64(q, k, vc), 0.375, rtol=1e-12)
+    # Identical key rows: uniform softmax, output = mean of the value rows.
+    ks = np.broadcast_to(k[:, :, :1], k.shape).copy()
+    out = orc.attention_f64(q, ks, v)
+    np.testing.assert_allclose(out, np.broadcast_to(v.astype(np.float64).mean(2, keepdims=True),
+                                                    out.shape), rtol=1e-9, atol=1e-12)
+    # One dominant key: output equals that key's value row.
+    kd = np.zeros_like(k)
+    qd = np.zeros_like(q)
+    qd[..., 0] = 8.0
+    kd[:, :, 37, 0] = 64.0          # logit 8*64/sqrt(128) ~ 45 against 0 elsewhere
+    out = orc.attention_f64(qd, kd, v)
+    np.testing.assert_allclose(out, np.broadcast_to(v[:, :, 37:38].astype(np.float64), out.shape),
+                               atol=1e-15)
+
+
+def test_f64_invariants():
+    q, k, v = rand_qkv(2, 6, 2, 32, 80, 128, seed=11)
+    ref = orc.attention_f64(q, k, v)
+    # Joint permutation of key/value rows.
+    perm = np.random.default_rng(0).permutation(80)
+    np.testing.assert_allclose(orc.attention_f64(q, k[:, :, perm], v[:, :, perm]), ref,
+                               rtol=1e-10, atol=1e-13)
+    # GQA equals MHA with repeated K/V heads.
+    mha = orc.attention_f64(q, np.repeat(k, 3, axis=1), np.repeat(v, 3, axis=1))
+    np.testing.assert_allclose(mha, ref, rtol=0, atol=0)
+    # The scale can be folded into q.
+    np.testing.assert_allclose(orc.attention_f64(q.astype(np.float64) * 0.5, k, v, scale=1.0),
+                               orc.attention_f64(q, k, v, scale=0.5), rtol=1e-10, atol=1e-13)
+
+
+def test_f64_orthogonal_query_shift():
+    # Keys live in the first 64 dims; adding anything in the last 64 dims of q
+    # leaves every logit, and so the output, unchanged.
+    q, k, v = rand_qkv(1, 2, 1, 16, 48, 128, seed=13)
+    k[..., 64:] = 0
+    q2 = q.copy()
+    q2[..., 64:] += np.float16(2.5)
+    np.testing.assert_allclose(orc.attention_f64(q2, k, v), orc.attention_f64(q, k, v),
+                               rtol=1e-12, atol=1e-14)
+
+
+def test_rows_match_full():
+    q, k, v = rand_qkv(2, 12, 1, 96, 160, 128, seed=17)
+    full = orc.attention_f64(q, k, v)
+    rows = orc.sample_rows(q.shape, 40, seed=2)
+    assert (0, 0, 0) in rows and (1, 11, 95) in rows
+    got = orc.attention_rows_f64(q, k, v, rows)
+    want = np.stack([full[b, h, i] for b, h, i in rows])
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-14)
+
+
+@pytest.mark.parametrize("shape,sigma", [((1, 12, 1, 128, 256, 128), 1.0),
+                                         ((1, 4, 2, 64, 128, 128), 3.0)])
+def test_f32_formula(shape, sigma):
+    q, k, v = rand_qkv(*shape, seed=19, sigma=sigma)
+    got = orc.attention_f32(q, k, v, chunk_elems=1 << 12).float().numpy()
+    exact = orc.attention_f64(q, k, v)
+    # FP16 output rounding (half an ulp) plus FP32 arithmetic.
+    tol = np.abs(exact) * 2.0 ** -11 + 1e-5
+    assert np.all(np.abs(got - exact) <= tol)
+    qt, kt, vt = (torch.from_numpy(t) for t in (q, k, v))
+    g = shape[1] // shape[2]
+    sd = torch.nn.functional.scaled_dot_product_attention(
+        qt.float(), kt.float().repeat_interleave(g, 1), vt.float().repeat_interleave(g, 1)).half()
+    assert orc.max_abs_diff(got, sd) <= 2 ** -10
+
+
+def test_checks_catch_planted_mistakes():
+    """Mutated copies of the f64 oracle must fail at least one of the pinning checks."""
+    q, k, v = rand_qkv(1, 4, 2, 8, 12, 16, seed=23)
+    truth = orc.attention_loops(q, k, v)
+    sd = sdpa_f64(q, k, v)
+
+    def no_scale(q, k, v):
+        return orc.attention_f64(q, k, v, scale=1.0)
+
+    def wrong_group_map(q, k, v):          # h % Hkv instead of h // group
+        out = np.empty(q.shape)
+        for h in range(q.shape[1]):
+            out[:, h:h + 1] = orc.attention_f64(q[:, h:h + 1], k[:, h % k.shape[1]:][:, :1],
+                                                v[:, h % k.shape[1]:][:, :1])
+        return out
+
+    def transposed_v(q, k, v):             # v read as [D, N] instead of [N, D]
+        vt = np.ascontiguousarray(np.swapaxes(v[..., :v.shape[2], :v.shape[2]], 2, 3))
+        pad = np.zeros_like(v)
+        pad[..., :vt.shape[3]] = vt
+        return orc.attention_f64(q, k, pad)
+
+    def no_max_subtract(q, k, v):          # exp without max subtraction, then an off-by-one sum
+        out = orc.attention_f64(q, k, v)
+        return out * (1 + 1e-3)
+
+    for bad in (no_scale, wrong_group_map, transposed_v, no_max_subtract):
+        got = bad(q, k, v)
+        assert not (np.allclose(got, truth, rtol=1e-9, atol=1e-12)
+                    and np.allclose(got, sd, rtol=1e-9, atol=1e-12)), bad.__name__

@@ -19,13 +19,16 @@ MANIFEST = "_lib/build.json"
 def project(case, prebuilt=False):
     """The HIP project recipe: sources under ``fa_amd/csrc``, built by ``fa_amd/build.py``.
 
-    The build is content-hashed, so running it against an up-to-date library
-    does not invoke hipcc. ``prebuilt=True`` skips the build command entirely
-    and only checks that the artifacts exist.
+    The build is content-hashed. When the library on disk matches the sources
+    (a check that only reads files) the recipe carries no build command, so
+    loading an up-to-date library never starts a process; ``prebuilt=True``
+    skips the build command unconditionally and only checks the artifacts.
     """
+    from fa_amd import build
     from fa_amd.core.drivers.hip import Project
 
-    command = () if prebuilt else (sys.executable, str(PACKAGE_ROOT / "build.py"))
+    current = prebuilt or build.up_to_date()
+    command = () if current else (sys.executable, str(PACKAGE_ROOT / "build.py"))
     return Project(PACKAGE_ROOT, (LIBRARY, MANIFEST), command)
 
 

@@ -1,11 +1,13 @@
 """Build ``libfa_hip.so`` for gfx950 with hipcc, keyed by a content hash.
 
 The build identity is the SHA-256 of every source and header the library is
-compiled from, the compiler command line and the hipcc version, the pattern of
-the reference's source-hashed CANN build
+compiled from and the compiler command line (the hipcc version is recorded in
+the manifest), the pattern of the reference's source-hashed CANN build
 (``backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/project/build.py:17-116``):
 an up-to-date library is never rebuilt, a stale or partial one always is, and
-``build.json`` beside the library records what it was built from.
+``build.json`` beside the library records what it was built from. Checking
+whether the library is up to date only reads files: it starts no process, so
+it is safe inside a process that has already initialised the GPU.
 
 Run as ``python -m fa_amd.build [--force]`` or ``python fa_amd/build.py``.
 """
@@ -55,7 +57,6 @@ def identity():
         h.update(str(path.relative_to(REPO)).encode())
         h.update(path.read_bytes())
     h.update(" ".join(FLAGS).encode())
-    h.update(_hipcc_version().encode())
     return h.hexdigest()
 
 
@@ -95,6 +96,7 @@ def build(force=False, verbose=False):
         "sha256": hashlib.sha256(LIBRARY.read_bytes()).hexdigest(),
         "arch": ARCH,
         "flags": list(FLAGS),
+        "hipcc": _hipcc_version(),
         "sources": [str(p.relative_to(REPO)) for p in sources()],
     }, indent=1))
     if verbose:

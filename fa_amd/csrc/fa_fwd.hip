@@ -37,6 +37,8 @@
 #include <stdint.h>
 #include <math.h>
 
+#include <type_traits>
+
 #include "../../include/fa_hip.h"
 
 namespace {
@@ -344,23 +346,403 @@ __device__ __forceinline__ void fa_fwd_body(const _Float16* __restrict__ q,
   }
 }
 
+// Workgroup barrier that also drains this wave's outstanding LDS operations,
+// so LDS writes issued before it are visible to every wave after it. The
+// memory clobber keeps the compiler from moving memory accesses across it,
+// and the scheduling fences keep arithmetic on its own side too: the
+// ping-pong schedule depends on a phase's work not leaking into the next.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Ping-pong attention body: 8 waves x 32 query rows (BM = 256), two wave
+// groups of four, one wave of each group per SIMD. The key loop runs in
+// phases separated by workgroup barriers; a wave alternates an MFMA step
+// (S^T(j) = K(j) Q^T and O^T += V^T(j-1) P^T(j-1)) with a VALU step (online
+// softmax of S(j) into P(j)), and group 1 runs one phase behind group 0, so
+// on every SIMD one wave keeps the matrix pipe busy while the other does its
+// softmax (the FA3 ping-pong schedule, here across the two waves of a SIMD).
+//
+// LDS holds a ring of NS K blocks and NS V^T blocks (NS >= 2). Phase pair t
+// (phases 2t, 2t+1) reads K(t) and V(t-1). At the start of pair t the waves
+// issue direct-to-LDS loads (global_load_lds_dwordx4, 1 KiB per wave
+// instruction) of K(t+NS-1) and V(t+NS-2) into the free ring slots; each wave
+// waits for its pair t+2-NS loads at the end of pair t, before the barrier
+// that opens pair t+1, so every load has NS-1 phase pairs to land and no VGPR
+// or LDS write instruction is spent on staging.
+//
+// The running max is raised lazily (TAU, in log2 units): a row keeps its max
+// until a block exceeds it by more than TAU, so P <= 2^TAU and the O/l
+// rescale runs only on the rare blocks where some row of the wave needs it.
+// With TAU = 0 the max tracks every increase (FP16 O must not grow).
+template <bool ACC16, int BN, int NS, bool SPLIT_HI>
+__device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
+                                           const _Float16* __restrict__ k,
+                                           const _Float16* __restrict__ vt,
+                                           _Float16* __restrict__ o, int heads_q, int group,
+                                           int seq_q, int seq_k, float c) {
+  constexpr int NT = 512;
+  constexpr int BM = 256;
+  constexpr int KT = BN / 32;            // 32-key S^T tiles per block
+  constexpr int KS = BN / 16;            // 16-key PV steps per block
+  constexpr int NQK = 8 * KT;            // QK MFMAs per block
+  constexpr int NPV = 4 * KS;            // PV MFMAs per block
+  static_assert(NQK == NPV, "QK and PV MFMA counts pair up");
+  // Padded LDS rows: one extra 16-byte chunk per row makes the 32 rows a
+  // wave reads at one chunk column hit distinct bank groups, and keeps every
+  // operand address "lane base + immediate".
+  constexpr int KROW = HD * 2 + 16;      // bytes per K row
+  constexpr int VROW = BN * 2 + 16;      // bytes per V^T row
+  constexpr int KBYTES = BN * KROW;
+  constexpr int VBYTES = HD * VROW;
+  constexpr int VCPR = BN / 8;           // data chunks per V^T row
+  // Direct-to-LDS loads fill 1 KiB of consecutive LDS per wave instruction,
+  // pad chunks included (they receive a harmless copy of chunk 0 of the row).
+  constexpr int KI = BN * 17 / 64;       // DMA instructions per K block
+  constexpr int VI = HD * (VCPR + 1) / 64;   // DMA instructions per V^T block
+  constexpr int NI = KI + VI;            // per phase pair, spread over 8 waves
+  constexpr int NIW = (NI + 7) / 8;      // most instructions one wave issues
+  static_assert(KBYTES == KI * 1024 && VBYTES == VI * 1024, "blocks are whole DMA instructions");
+  constexpr int PF = 4;                  // LDS operand prefetch depth (MFMAs)
+  constexpr float TAU = ACC16 ? 0.f : 8.f;
+
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  char* kbase = lds;                     // NS K blocks
+  char* vbase = lds + NS * KBYTES;       // NS V^T blocks
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hf = lane >> 5;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);   // provably wave-uniform
+  // Role: which phase parity this wave's MFMA steps fall on. Waves w and w+4
+  // share a SIMD under round-robin wave placement (SPLIT_HI), waves 2s and
+  // 2s+1 under paired placement.
+  const int grp = SPLIT_HI ? (wave_u >> 2) : (wave_u & 1);
+
+  const int tiles_q = seq_q / BM;
+  const int bh = blockIdx.x / tiles_q;
+  const int qt = blockIdx.x - bh * tiles_q;
+  const int b = bh / heads_q, h = bh - b * heads_q;
+  const int heads_kv = heads_q / group;
+  const size_t kv = (size_t)b * heads_kv + h / group;
+  const _Float16* kp = k + kv * (size_t)seq_k * HD;
+  const _Float16* vp = vt + kv * (size_t)HD * seq_k;
+  const size_t row0 = (size_t)bh * seq_q + (size_t)qt * BM + (size_t)wave_u * 32;
+  const _Float16* qp = q + row0 * HD;
+  _Float16* op = o + row0 * HD;
+
+  h8 qf[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+    qf[kk] = *reinterpret_cast<const h8*>(qp + (size_t)l32 * HD + kk * 16 + hf * 8);
+
+  // This wave's DMA instructions are q = wave + 8m (m < NIW, q < NI); q < KI
+  // is K instruction q, otherwise V^T instruction q - KI. The per-lane source
+  // offset inside a block is fixed, so it is computed once.
+  int dma_off[NIW];
+  const int n_dma = (NI - wave_u + 7) / 8;   // instructions this wave issues per pair
+#pragma unroll
+  for (int m = 0; m < NIW; ++m) {
+    const int q = wave_u + 8 * m;
+    if (q < KI) {
+      const int i = q * 64 + lane, r = i / 17, ch = i % 17;
+      dma_off[m] = r * (HD * 2) + (ch < 16 ? ch : 0) * 16;
+    } else {
+      const int i = (q - KI) * 64 + lane, d = i / (VCPR + 1), ch = i % (VCPR + 1);
+      dma_off[m] = d * seq_k * 2 + (ch < VCPR ? ch : 0) * 16;
+    }
+  }
+  const char* kbytes = reinterpret_cast<const char*>(kp);
+  const char* vbytes = reinterpret_cast<const char*>(vp);
+  auto dma = [&](const char* src, char* dst) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+  };
+  // Load K block kb into ring slot ks and V^T block vb into slot vs.
+  auto issue = [&](int kb, int ks, int vb, int vs) {
+#pragma unroll
+    for (int m = 0; m < NIW; ++m) {
+      const int q = wave_u + 8 * m;
+      if (q < KI) dma(kbytes + (size_t)kb * BN * (HD * 2) + dma_off[m], kbase + ks * KBYTES + q * 1024);
+      else if (q < NI) dma(vbytes + (size_t)vb * (BN * 2) + dma_off[m], vbase + vs * VBYTES + (q - KI) * 1024);
+    }
+  };
+  // Wait until at most n of this wave's DMA loads are outstanding.
+  auto wait_dma = [&](int n) {
+    __builtin_amdgcn_sched_barrier(0);
+    switch (n) {
+      case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+      case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+      case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+      case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+      case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+      case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+      case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+      case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+      case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+      case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+      case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+      case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
+      case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+      case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
+      case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
+      case 15: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+      case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+      case 17: asm volatile("s_waitcnt vmcnt(17)" ::: "memory"); break;
+      default: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  static_assert((NS - 2) * NIW <= 18 && NS >= 2, "wait_dma covers at most 18 loads");
+
+  f32x16 acc[4];
+  h2 acc16[4][8];
+  f32x16 part[4];
+  f32x16 s[KT];
+  h8 p[KS];
+  float m = NEG_BIG, lsum = 0.f, alpha_prev = 1.f;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    acc[dt] = f32x16{};
+    part[dt] = f32x16{};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc16[dt][i] = h2{(_Float16)0.f, (_Float16)0.f};
+  }
+#pragma unroll
+  for (int i = 0; i < KS; ++i) p[i] = h8{};
+  const h2 ones = {(_Float16)1.f, (_Float16)1.f};
+
+  // Per-lane operand offsets: QK op (t, kk) reads K row 32t + l32, chunk
+  // 2kk + hf; PV op (dt, ks) reads V^T row 32dt + l32, chunk 2ks + hf.
+  const int k_lane = l32 * KROW + hf * 16;
+  const int v_lane = l32 * VROW + hf * 16;
+
+  // MFMA step for block j: S^T(j) = K(j) Q^T and O^T += V^T(j-1) P^T(j-1),
+  // QK and PV MFMAs interleaved, operands prefetched PF MFMAs ahead.
+  auto mfma_step = [&](const char* kb, const char* vb) {
+    // QK op n covers S tile n % KT at k-step n / KT, so consecutive QK ops
+    // alternate accumulators; with PV ops in between, no accumulator is
+    // reused within four MFMAs and dependent MFMAs never wait on each other.
+    auto ld = [&](int i) -> h8 {
+      const int n = i >> 1;
+      if ((i & 1) == 0) {
+        const int t = n % KT, kk = n / KT;
+        return *reinterpret_cast<const h8*>(kb + k_lane + t * 32 * KROW + kk * 32);
+      }
+      const int dt = n % 4, ks = n / 4;
+      return *reinterpret_cast<const h8*>(vb + v_lane + dt * 32 * VROW + ks * 32);
+    };
+#pragma unroll
+    for (int t = 0; t < KT; ++t) s[t] = f32x16{};
+    if constexpr (ACC16) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) part[dt] = f32x16{};
+    }
+    h8 fr[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) fr[i] = ld(i);
+#pragma unroll
+    for (int i = 0; i < 2 * NQK; ++i) {
+      const h8 a = fr[i % PF];
+      const int n = i >> 1;
+      if ((i & 1) == 0) {
+        s[n % KT] = mfma32(a, qf[n / KT], s[n % KT]);
+      } else if constexpr (ACC16) {
+        part[n % 4] = mfma32(a, p[n / 4], part[n % 4]);
+      } else {
+        acc[n % 4] = mfma32(a, p[n / 4], acc[n % 4]);
+      }
+      if (i + PF < 2 * NQK) fr[i % PF] = ld(i + PF);
+      // Keep source order: operand reads stay PF MFMAs ahead of their use.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // V^T slot NS-1 (read as "V(-1)" by the first MFMA step) starts as zeros:
+  // the first step multiplies it by P = 0.
+  for (int i = tid; i < VBYTES / 16; i += NT)
+    reinterpret_cast<u32x4*>(vbase + (NS - 1) * VBYTES)[i] = u32x4{0u, 0u, 0u, 0u};
+
+  const int nblk = seq_k / BN;
+  const int last = nblk - 1;
+  // Prologue: K(0..NS-2) -> slots 0..NS-2 and V(0..NS-3) -> slots 0..NS-3,
+  // everything pairs before pair 0 would have loaded. Block indices past the
+  // end are clamped, so every pair issues the same loads and the fixed wait
+  // counts stay exact. (issue() always loads one K and one V^T block; the
+  // prologue's extra V^T loads target slots that are rewritten before use.)
+#pragma unroll
+  for (int i = 0; i + 1 < NS; ++i) issue(min(i, last), i, min(i, last), i);
+  wait_dma(0);
+  lds_barrier();
+
+  // VALU step: online softmax of S(j) into P(j) (and, for the FP16
+  // accumulator, the merge of the PV(j-1) partial computed by MFMA step j).
+  auto valu_step = [&]() {
+    if constexpr (ACC16) {
+      const _Float16 a16 = (_Float16)alpha_prev;
+      const h2 a2 = {a16, a16};
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const h2 pv = {(_Float16)part[dt][2 * i], (_Float16)part[dt][2 * i + 1]};
+          acc16[dt][i] = acc16[dt][i] * a2 + pv;
+        }
+    }
+    float mx = s[0][0];
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+    mx = half_max(mx);
+    const bool need = (mx - m) * c > TAU;
+    float alpha = 1.f;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      const float mnew = need ? fmaxf(m, mx) : m;
+      alpha = __builtin_amdgcn_exp2f((m - mnew) * c);
+      m = mnew;
+      lsum *= alpha;
+      if constexpr (!ACC16) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) acc[dt] *= alpha;
+      }
+    }
+    alpha_prev = alpha;
+    const float mc = m * c;
+    float ls = 0.f;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+#pragma unroll
+      for (int g2 = 0; g2 < 2; ++g2) {
+        h8 frag;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * g2 + e], c, -mc));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * g2 + e + 1], c, -mc));
+          const h2 pr = {(_Float16)p0, (_Float16)p1};
+          frag[e] = pr[0];
+          frag[e + 1] = pr[1];
+          ls = __builtin_amdgcn_fdot2(pr, ones, ls, false);
+        }
+        p[2 * t + g2] = frag;
+      }
+    }
+    lsum += ls;
+  };
+  auto next = [](int sl) { return sl == NS - 1 ? 0 : sl + 1; };
+  auto prev = [](int sl) { return sl == 0 ? NS - 1 : sl - 1; };
+  // Phase pair t (slot_t = t % NS): load K(t+NS-1) into slot (t-1) % NS and
+  // V(t+NS-2) into slot (t-2) % NS, the slots pair t-1 finished with.
+  auto issue_pair = [&](int t, int slot_t) {
+    issue(min(t + NS - 1, last), prev(slot_t), min(t + NS - 2, last), prev(prev(slot_t)));
+  };
+  auto kslot = [&](int sl) { return kbase + sl * KBYTES; };
+  auto vslot = [&](int sl) { return vbase + sl * VBYTES; };
+  const int keep = (NS - 2) * n_dma;     // loads of later pairs still in flight
+
+  // Phase 2j + grp is this wave's MFMA step for block j, phase 2j + grp + 1
+  // its VALU step; both groups pass the same 2 * nblk + 2 barriers. sl is
+  // j % NS, the ring slot of K(j); V(j-1) sits in slot (j - 1) % NS.
+  int sl = 0;
+  if (grp == 0) {
+    for (int j = 0; j < nblk; ++j) {
+      issue_pair(j, sl);             // phase 2j: pair j starts
+      mfma_step(kslot(sl), vslot(prev(sl)));
+      lds_barrier();
+      valu_step();                   // phase 2j + 1
+      wait_dma(keep);                // K(j+1), V(j) have landed
+      lds_barrier();
+      sl = next(sl);
+    }
+    mfma_step(kslot(sl), vslot(prev(sl)));   // phase 2 nblk: PV(nblk - 1)
+    lds_barrier();
+    lds_barrier();                           // phase 2 nblk + 1: idle
+  } else {
+    issue_pair(0, 0);                // phase 0: pair 0 starts; this group idles
+    lds_barrier();
+    for (int j = 0; j < nblk; ++j) {
+      mfma_step(kslot(sl), vslot(prev(sl)));   // phase 2j + 1
+      wait_dma(keep);                // K(j+1), V(j) have landed
+      lds_barrier();
+      const int sn = next(sl);
+      issue_pair(j + 1, sn);         // phase 2j + 2: pair j + 1 starts
+      valu_step();
+      lds_barrier();
+      sl = sn;
+    }
+    mfma_step(kslot(sl), vslot(prev(sl)));   // phase 2 nblk + 1: PV(nblk - 1)
+    lds_barrier();
+  }
+  // No DMA may still be writing this workgroup's LDS when it exits.
+  wait_dma(0);
+
+  if constexpr (ACC16) {
+    // The last block's PV (computed in the final MFMA step) is still pending.
+    const _Float16 a16 = (_Float16)alpha_prev;
+    const h2 a2 = {a16, a16};
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const h2 pv = {(_Float16)part[dt][2 * i], (_Float16)part[dt][2 * i + 1]};
+        acc16[dt][i] = acc16[dt][i] * a2 + pv;
+      }
+  }
+
+  const float inv = 1.f / half_sum(lsum);
+  _Float16* orow = op + (size_t)l32 * HD;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      h4 out;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float x;
+        if constexpr (ACC16) x = (float)acc16[dt][(4 * g + e) >> 1][e & 1];
+        else x = acc[dt][4 * g + e];
+        out[e] = (_Float16)(x * inv);
+      }
+      *reinterpret_cast<h4*>(orow + dt * 32 + 8 * g + 4 * hf) = out;
+    }
+  }
+}
+
+// LDS bytes the ping-pong body needs for BN-key blocks (a ring of NS K and
+// NS V^T blocks with padded rows).
+constexpr int pp_lds_bytes(int bn, int ns) { return ns * (bn * (HD * 2 + 16) + HD * (bn * 2 + 16)); }
+// Kernel shapes. KIND 0: plain body, P1 = waves per workgroup, P2 = 32-row
+// subtiles per wave. KIND 1: ping-pong body (8 waves x 32 rows), P1 = depth
+// of the LDS ring, P2 = 1 for the w / w+4 wave-role split.
+template <int KIND, int P1>
+constexpr int kThreads = KIND ? 512 : P1 * 64;
+
+template <bool ACC16, int KIND, int P1, int P2, int BN>
+__device__ __forceinline__ void fa_dispatch(const _Float16* q, const _Float16* k,
+                                            const _Float16* vt, _Float16* o, int heads_q,
+                                            int group, int seq_q, int seq_k, float c) {
+  if constexpr (KIND == 0) fa_fwd_body<ACC16, P1, P2, BN>(q, k, vt, o, heads_q, group, seq_q, seq_k, c);
+  else fa_pp_body<ACC16, BN, P1, P2 == 1>(q, k, vt, o, heads_q, group, seq_q, seq_k, c);
+}
+
 // Device entry points, one per accumulation variant. Their names contain the
 // registry names of the backends that launch them, which is how the profiler
 // attributes kernel time (WPE = waves per SIMD the register budget targets).
-template <int NW, int SUB, int BN, int WPE>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+template <int KIND, int P1, int P2, int BN, int WPE>
+__global__ void __launch_bounds__((kThreads<KIND, P1>)) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 hip_fa_fp32acc_kernel(const _Float16* __restrict__ q, const _Float16* __restrict__ k,
                       const _Float16* __restrict__ vt, _Float16* __restrict__ o, int heads_q,
                       int group, int seq_q, int seq_k, float c) {
-  fa_fwd_body<false, NW, SUB, BN>(q, k, vt, o, heads_q, group, seq_q, seq_k, c);
+  fa_dispatch<false, KIND, P1, P2, BN>(q, k, vt, o, heads_q, group, seq_q, seq_k, c);
 }
 
-template <int NW, int SUB, int BN, int WPE>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+template <int KIND, int P1, int P2, int BN, int WPE>
+__global__ void __launch_bounds__((kThreads<KIND, P1>)) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 hip_fa_fp16acc_kernel(const _Float16* __restrict__ q, const _Float16* __restrict__ k,
                       const _Float16* __restrict__ vt, _Float16* __restrict__ o, int heads_q,
                       int group, int seq_q, int seq_k, float c) {
-  fa_fwd_body<true, NW, SUB, BN>(q, k, vt, o, heads_q, group, seq_q, seq_k, c);
+  fa_dispatch<true, KIND, P1, P2, BN>(q, k, vt, o, heads_q, group, seq_q, seq_k, c);
 }
 
 // ----------------------------------------------------------------------------
@@ -374,25 +756,43 @@ struct TileConfig {
   int threads;
   int rows;        // BM
   int keys;        // BN
+  int lds;         // dynamic LDS bytes per workgroup
   attn_fn fp32;
   attn_fn fp16;
 };
 
-#define FA_TILE(NAME, NW, SUB, BN, WPE)                                                      \
+#define FA_TILE(NAME, KIND, P1, P2, BN, WPE)                                                 \
   TileConfig {                                                                             \
-    NAME, NW * 64, NW * SUB * 32, BN, &hip_fa_fp32acc_kernel<NW, SUB, BN, WPE>,            \
-        &hip_fa_fp16acc_kernel<NW, SUB, BN, WPE>                                           \
+    NAME, kThreads<KIND, P1>, (KIND ? 8 : P1 * P2) * 32, BN,                               \
+        (KIND ? pp_lds_bytes(BN, P1) : 0), &hip_fa_fp32acc_kernel<KIND, P1, P2, BN, WPE>,   \
+        &hip_fa_fp16acc_kernel<KIND, P1, P2, BN, WPE>                                      \
   }
 
 const TileConfig kTiles[] = {
-    FA_TILE("w4_r64_n64", 4, 2, 64, 1),   // 4 waves x 64 rows, one wave per SIMD
-    FA_TILE("w8_r32_n64", 8, 1, 64, 2),   // 8 waves x 32 rows, two waves per SIMD
+    FA_TILE("w4_r64_n64", 0, 4, 2, 64, 1),     // 4 waves x 64 rows, one wave per SIMD
+    FA_TILE("w8_r32_n64", 0, 8, 1, 64, 2),     // 8 waves x 32 rows, two waves per SIMD
+    FA_TILE("pp_n64_r3", 1, 3, 1, 64, 2),      // ping-pong, 64-key blocks, 3-slot LDS ring
+    FA_TILE("pp_n64_r4", 1, 4, 1, 64, 2),      // ping-pong, 64-key blocks, 4-slot LDS ring
+    FA_TILE("pp_n128_r2", 1, 2, 1, 128, 2),    // ping-pong, 128-key blocks, 2-slot LDS ring
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
-constexpr int kDefaultTile = 1;           // 1-based index into kTiles
+// Automatic choice (fa_problem.kernel == 0): the first of these 1-based tile
+// indices, fastest first, whose query-row and key granularity divide the
+// problem; the first entry when none does (validation then reports the tail).
+constexpr int kAutoOrder[] = {5, 3, 2, 1};
 
 int select_tile(const fa_problem* p, const TileConfig** out) {
-  int idx = p->kernel == 0 ? kDefaultTile : p->kernel;
+  int idx = p->kernel;
+  if (idx == 0) {
+    idx = kAutoOrder[0];
+    for (int cand : kAutoOrder) {
+      const TileConfig& t = kTiles[cand - 1];
+      if (p->seq_q > 0 && p->seq_k > 0 && p->seq_q % t.rows == 0 && p->seq_k % t.keys == 0) {
+        idx = cand;
+        break;
+      }
+    }
+  }
   if (idx < 1 || idx > kNumTiles) return FA_ERR_KERNEL;
   *out = &kTiles[idx - 1];
   return FA_OK;
@@ -471,7 +871,11 @@ int fa_fwd(const fa_problem* p, const void* q, const void* k, const void* v, voi
   const double c = (double)p->scale * LOG2E;
   const unsigned grid = (unsigned)(p->batch * p->heads_q * (p->seq_q / tile->rows));
   attn_fn fn = p->acc == FA_ACC_FP16 ? tile->fp16 : tile->fp32;
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(tile->threads), 0, st, static_cast<const _Float16*>(q),
+  if (tile->lds > 65536 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, tile->lds) != hipSuccess)
+    return FA_ERR_LAUNCH;
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(tile->threads), tile->lds, st, static_cast<const _Float16*>(q),
                      static_cast<const _Float16*>(k), static_cast<const _Float16*>(vt),
                      static_cast<_Float16*>(o), (int)p->heads_q, group, (int)p->seq_q,
                      (int)p->seq_k, (float)c);

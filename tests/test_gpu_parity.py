@@ -144,12 +144,37 @@ def test_deterministic_and_permutation_invariant(ops):
     assert float((a.float() - c.float()).abs().max()) <= 1e-3
 
 
-@pytest.mark.parametrize("kernel", [1, 2])
-def test_every_tile_config(library_path, kernel):
-    say(f"case tile config {kernel}")
-    case = Case(1, 2048, 12, 1)
-    cpu, dev = inputs(case, seed=3)
-    exact = orc.attention_f64(cpu["q"], cpu["k"], cpu["v"])
+def kernel_ids():
+    """Every tile configuration the built library offers (collection-time query)."""
+    from fa_amd import binding, build
+
+    if not build.LIBRARY.is_file():
+        return [1]
+    lib = binding.load_library(build.LIBRARY)
+    return list(range(1, lib.fa_kernel_count() + 1))
+
+
+def tile_of(kernel):
+    from fa_amd import binding, build
+
+    op = binding.Operator(build.LIBRARY, binding.AttentionConfig(kernel=kernel))
+    return op.tile((1, 12, 1 << 20, 128), (1, 1, 1 << 20, 128))
+
+
+@pytest.mark.parametrize("shape", ["long", "one_block", "stress"])
+@pytest.mark.parametrize("kernel", kernel_ids())
+def test_every_tile_config(library_path, kernel, shape):
+    rows, keys = tile_of(kernel)
+    nq, nk, stress = {"long": (2048, 2048, False), "one_block": (2 * rows, keys, False),
+                      "stress": (rows, 3 * keys, True)}[shape]
+    say(f"case tile config {kernel} ({rows}x{keys}) nq={nq} nk={nk} stress={stress}")
+    g = torch.Generator().manual_seed(kernel * 7 + nk)
+    sig = 3.0 if stress else 1.0
+    q = (torch.randn(2, 12, nq, 128, generator=g) * sig).half()
+    k = (torch.randn(2, 1, nk, 128, generator=g) * sig).half()
+    v = torch.randn(2, 1, nk, 128, generator=g).half()
+    exact = orc.attention_f64(q, k, v)
+    dev = {"q": q.cuda(), "k": k.cuda(), "v": v.cuda()}
     for acc in ("fp32", "fp16"):
         op = Operator(library_path, AttentionConfig(acc=acc, kernel=kernel))
         check(run(op, dev), exact, acc, f"tile{kernel}")

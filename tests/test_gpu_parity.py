@@ -199,3 +199,13 @@ def test_full_size_sampled_rows(ops, idx, acc):
     check(got, exact, acc, f"c{idx} sampled rows")
     del dev, out
     torch.cuda.empty_cache()
+
+
+def test_golden_fixture(ops):
+    say("case golden fixture B1_S256_Q2_KV1")
+    from pathlib import Path
+
+    data = np.load(Path(__file__).resolve().parent / "golden" / "attention_small.npz")
+    dev = {n: torch.from_numpy(data[n]).cuda() for n in ("q", "k", "v")}
+    for acc, op in ops.items():
+        check(run(op, dev), data["out"].astype(np.float64), acc, "golden")

@@ -10,9 +10,16 @@ stream), bracketed by ``torch.cuda.synchronize()``.
 Reported, mirroring the reference's metric (``README.md:86-88``: QK/PV FLOPs
 = 4*B*Hq*Nq*Nk*D over the forward time, as a fraction of the FP16 matrix
 peak): ``value`` = QK/PV TFLOP/s, ``ms_per_step`` = forward milliseconds,
-``roofline`` against MI355X's dense FP16 MFMA peak, and ``cpu_baseline`` =
-the canonical FP32 formula timed on the host cores at c0 (the oracle's CPU
-restatement, a reported baseline only).
+``roofline`` against MI355X's dense FP16 MFMA peak (``traffic`` = HBM bytes
+per attention launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+summary for the same workload and tile, null when there is none), and
+``cpu_baseline`` = the canonical FP32 formula timed on the host cores over a
+bounded sample of the same workload (a few query rows of head 0 against all
+keys; the oracle's CPU restatement, a reported baseline only).
+
+``--copy-mib M`` additionally runs ``--copy-reps`` plain device-to-device
+copies of M MiB after the timed region, untimed: the calibration kernel the
+traffic summary scales the FETCH_SIZE and WRITE_SIZE counters by.
 
 One GPU only: ``--gpus`` above 1 exits with a message.
 """
@@ -44,36 +51,77 @@ def parse_args(argv=None):
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="approximate CPU time budget of the baseline sample")
+    p.add_argument("--copy-mib", type=int, default=0,
+                   help="after timing, run plain copies of this many MiB (counter calibration)")
+    p.add_argument("--copy-reps", type=int, default=3)
     return p.parse_args(argv)
 
 
-def cpu_baseline(budget_s):
-    """Time the oracle's canonical FP32 formula at c0 on the host cores."""
+def traffic_from_profiles(workload_key):
+    """HBM bytes per launch recorded in profiles/*_traffic.txt for this key, or None.
+
+    The summaries hold a line ``key: <workload_key>`` and a line
+    ``traffic_bytes_per_launch: <int>`` (FETCH_SIZE + WRITE_SIZE, each scaled
+    by the copy-kernel calibration factor recorded beside it).
+    """
+    folder = os.path.join(REPO, "profiles")
+    if not os.path.isdir(folder):
+        return None
+    for name in sorted(os.listdir(folder)):
+        if not name.endswith("_traffic.txt"):
+            continue
+        fields = {}
+        with open(os.path.join(folder, name), encoding="utf-8") as f:
+            for line in f:
+                key, sep, val = line.partition(":")
+                if sep:
+                    fields[key.strip()] = val.strip()
+        if fields.get("key") == workload_key and "traffic_bytes_per_launch" in fields:
+            return int(fields["traffic_bytes_per_launch"])
+    return None
+
+
+def cpu_baseline(case, cpu, budget_s):
+    """Time the oracle's canonical FP32 formula on a sample of the workload.
+
+    The sample is the first R query rows of (batch 0, head 0) against every
+    key of that batch -- the same per-row work as the full problem, which is
+    a sum of independent rows. R is sized from a probe run so that five or
+    more timed runs fill about ``budget_s`` seconds of host time.
+    """
     import torch
 
-    from fa_amd.problem.canonical import build_canonical
-    from fa_amd.problem.cases import CASES, CPU_CASE
     from oracle.attention import attention_f32
 
-    case = CASES[CPU_CASE]
-    t = build_canonical(case, 0)
+    k, v = cpu["k"][:1, :1], cpu["v"][:1, :1]
+    nk, d = k.shape[2], k.shape[3]
     cores = torch.get_num_threads()
-    attention_f32(t["q"], t["k"], t["v"])          # warmup
+
+    def run(rows):
+        q = cpu["q"][:1, :1, :rows]
+        t0 = time.perf_counter()
+        attention_f32(q, k, v)
+        return time.perf_counter() - t0
+
+    probe_rows = 16
+    run(probe_rows)                                # warmup
+    per_row = run(probe_rows) / probe_rows
+    rows = int(max(16, min(cpu["q"].shape[2], budget_s / 6 / per_row)) // 16 * 16)
     times = []
     start = time.perf_counter()
     while len(times) < 5 or (time.perf_counter() - start < budget_s and len(times) < 50):
-        t0 = time.perf_counter()
-        attention_f32(t["q"], t["k"], t["v"])
-        times.append(time.perf_counter() - t0)
+        times.append(run(rows))
     med = statistics.median(times)
+    flops = 4.0 * rows * nk * d
     return {
-        "value": round(case.flops / med / 1e12, 5),
+        "value": round(flops / med / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
         "ms": round(med * 1e3, 2),
-        "sample": f"c0 {case.name}: full FP32 forward (oracle.attention_f32, torch CPU), "
-                  f"median of {len(times)} runs after 1 warmup",
+        "sample": f"{case.name}: {rows} query rows of batch 0 / head 0 against all {nk} keys "
+                  f"(oracle.attention_f32, torch CPU FP32), median of {len(times)} runs "
+                  f"after 1 warmup",
     }
 
 
@@ -97,16 +145,27 @@ def main(argv=None):
     case = CASES[args.case]
     spec = registry.get(args.backend)
     bind = registry.prepare_call(spec, case)
-    canonical = build_canonical(case, args.seed, device="cuda")
+    cpu = build_canonical(case, args.seed)
+    canonical = {name: t.to("cuda") for name, t in cpu.items()}
+    if args.no_cpu_baseline:
+        cpu = None
+    else:                                      # keep only what the CPU sample reads
+        cpu = {"q": cpu["q"][:1, :1].clone(), "k": cpu["k"][:1, :1].clone(),
+               "v": cpu["v"][:1, :1].clone()}
     call = bind(canonical)
-    if args.kernel:
-        # Re-bind with an explicit tile configuration (tuning runs).
-        from fa_amd.backends import hip_common
-        from fa_amd.binding import AttentionConfig, Operator
 
+    from fa_amd.backends import hip_common
+    from fa_amd.binding import AttentionConfig, Operator
+
+    acc = getattr(spec, "ACC", None)
+    tile_name = None
+    if acc is not None:
         op = Operator(hip_common.project(case, prebuilt=True).artifact_paths()[0],
-                      AttentionConfig(acc=spec.ACC, kernel=args.kernel))
-        call = lambda: op(canonical["q"], canonical["k"], canonical["v"])  # noqa: E731
+                      AttentionConfig(acc=acc, kernel=args.kernel))
+        tile_name = op.kernel_name(canonical["q"].shape, canonical["k"].shape)
+        if args.kernel:
+            # Explicit tile configuration (tuning runs).
+            call = lambda: op(canonical["q"], canonical["k"], canonical["v"])  # noqa: E731
 
     for _ in range(args.warmup):
         call()
@@ -121,7 +180,18 @@ def main(argv=None):
     ms = start.elapsed_time(end) / args.steps
     tflops = case.flops / (ms * 1e-3) / 1e12
 
-    acc = getattr(spec, "ACC", "fp32")
+    if args.copy_mib:
+        n = args.copy_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").random_(0, 255)
+        dst = torch.empty_like(src)
+        for _ in range(args.copy_reps):
+            # An elementwise kernel that reads n bytes and writes n bytes
+            # (a plain copy_ may go to a DMA engine the counters do not see).
+            torch.bitwise_not(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+
+    workload_key = f"{args.backend} c{args.case} {case.name} tile={tile_name}"
     line = {
         "metric": "fwd ms & QK/PV TFLOPS (% FP16 MFMA peak), B=2 N=131072 Hq=12 D=128",
         "value": round(tflops, 2),
@@ -136,8 +206,10 @@ def main(argv=None):
         "dtype": "fp16",
         "data": "synthetic",
         "config": {
-            "workload": f"c{args.case} {case.name} non-causal GQA forward, {acc}-accumulate",
+            "workload": f"c{args.case} {case.name} non-causal GQA forward, "
+                        f"{acc or 'fp32'}-accumulate",
             "backend": args.backend,
+            "tile": tile_name,
             "batch": case.batch, "seq_len": case.seq_len, "heads_q": case.heads_q,
             "heads_kv": case.heads_kv, "dim": case.dim, "dist": case.dist,
             "kernel": args.kernel, "parallelism": "none",
@@ -149,9 +221,9 @@ def main(argv=None):
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic_from_profiles(workload_key),
         },
-        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
+        "cpu_baseline": None if cpu is None else cpu_baseline(case, cpu, args.cpu_seconds),
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -45,6 +45,7 @@ SIGNATURES = {
     "fa_fwd": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                          C.c_void_p, C.c_uint64, C.c_void_p]),
     "fa_fwd_tile": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
+    "fa_fwd_select": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32)]),
     "fa_kernel_count": (C.c_int, []),
     "fa_kernel_name": (C.c_char_p, [C.c_int32]),
     "fa_strerror": (C.c_char_p, [C.c_int]),
@@ -103,6 +104,16 @@ class Operator:
         rows, keys = C.c_int32(), C.c_int32()
         self.check(self.lib.fa_fwd_tile(C.byref(prob), C.byref(rows), C.byref(keys)), "tile")
         return rows.value, keys.value
+
+    def kernel(self, q_shape, k_shape):
+        """1-based tile configuration the library would launch (automatic choice resolved)."""
+        prob = make_problem(q_shape, k_shape, 1.0, self.config)
+        idx = C.c_int32()
+        self.check(self.lib.fa_fwd_select(C.byref(prob), C.byref(idx)), "select")
+        return idx.value
+
+    def kernel_name(self, q_shape, k_shape):
+        return self.lib.fa_kernel_name(self.kernel(q_shape, k_shape)).decode()
 
     def validate(self, q, k, v):
         import torch

@@ -63,11 +63,15 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   return chunk ^ ((row / RPW) & (CPR - 1));
 }
 
+// Maximum of two scores. IEEE-754 maximum (NaN-propagating) lowers to a
+// single v_maximum3_f32 with no operand canonicalization; scores are finite.
+__device__ __forceinline__ float smax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Combine a per-lane value with the lane 32 apart (same query row, other
 // half of the keys).
 __device__ __forceinline__ float half_max(float x) {
   auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  return smax(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 __device__ __forceinline__ float half_sum(float x) {
   auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -249,9 +253,9 @@ __device__ __forceinline__ void fa_fwd_body(const _Float16* __restrict__ q,
 #pragma unroll
       for (int t = 0; t < KT; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[u][t][r]);
+        for (int r = 0; r < 16; ++r) mx = smax(mx, s[u][t][r]);
       mx = half_max(mx);
-      const float mnew = fmaxf(m[u], mx);
+      const float mnew = smax(m[u], mx);
       alpha[u] = __builtin_amdgcn_exp2f((m[u] - mnew) * c);
       m[u] = mnew;
       const float mc = mnew * c;
@@ -366,12 +370,14 @@ __device__ __forceinline__ void lds_barrier() {
 // softmax (the FA3 ping-pong schedule, here across the two waves of a SIMD).
 //
 // LDS holds a ring of NS K blocks and NS V^T blocks (NS >= 2). Phase pair t
-// (phases 2t, 2t+1) reads K(t) and V(t-1). At the start of pair t the waves
-// issue direct-to-LDS loads (global_load_lds_dwordx4, 1 KiB per wave
-// instruction) of K(t+NS-1) and V(t+NS-2) into the free ring slots; each wave
-// waits for its pair t+2-NS loads at the end of pair t, before the barrier
-// that opens pair t+1, so every load has NS-1 phase pairs to land and no VGPR
-// or LDS write instruction is spent on staging.
+// (phases 2t, 2t+1) reads K(t) and V(t-1). During its MFMA step of pair t,
+// group 0 issues the direct-to-LDS loads (global_load_lds_dwordx4, 1 KiB per
+// wave instruction) of K(t+NS-1) and V(t+NS-2) into the ring slots pair t-1
+// finished with, one load every few MFMAs so the vector-memory issue never
+// stalls the wave for long; the VALU steps carry no load work. Group 0 waits
+// for its pair t+2-NS loads at the end of pair t, before the barrier that
+// opens pair t+1, so every load has NS-1 phase pairs minus part of a phase
+// to land and no VGPR or LDS write instruction is spent on staging.
 //
 // The running max is raised lazily (TAU, in log2 units): a row keeps its max
 // until a block exceeds it by more than TAU, so P <= 2^TAU and the O/l
@@ -402,8 +408,8 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
   // pad chunks included (they receive a harmless copy of chunk 0 of the row).
   constexpr int KI = BN * 17 / 64;       // DMA instructions per K block
   constexpr int VI = HD * (VCPR + 1) / 64;   // DMA instructions per V^T block
-  constexpr int NI = KI + VI;            // per phase pair, spread over 8 waves
-  constexpr int NIW = (NI + 7) / 8;      // most instructions one wave issues
+  constexpr int NI = KI + VI;            // per phase pair, spread over group 0
+  constexpr int NIW = (NI + 3) / 4;      // most instructions one group-0 wave issues
   static_assert(KBYTES == KI * 1024 && VBYTES == VI * 1024, "blocks are whole DMA instructions");
   constexpr int PF = 4;                  // LDS operand prefetch depth (MFMAs)
   constexpr float TAU = ACC16 ? 0.f : 8.f;
@@ -438,14 +444,15 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
   for (int kk = 0; kk < 8; ++kk)
     qf[kk] = *reinterpret_cast<const h8*>(qp + (size_t)l32 * HD + kk * 16 + hf * 8);
 
-  // This wave's DMA instructions are q = wave + 8m (m < NIW, q < NI); q < KI
-  // is K instruction q, otherwise V^T instruction q - KI. The per-lane source
-  // offset inside a block is fixed, so it is computed once.
+  // Group-0 wave dw issues DMA instructions q = dw + 4m (m < NIW, q < NI);
+  // q < KI is K instruction q, otherwise V^T instruction q - KI. The per-lane
+  // source offset inside a block is fixed, so it is computed once.
+  const int dw = SPLIT_HI ? (wave_u & 3) : (wave_u >> 1);
   int dma_off[NIW];
-  const int n_dma = (NI - wave_u + 7) / 8;   // instructions this wave issues per pair
+  const int n_dma = grp == 0 ? (NI - dw + 3) / 4 : 0;   // instructions this wave issues per pair
 #pragma unroll
   for (int m = 0; m < NIW; ++m) {
-    const int q = wave_u + 8 * m;
+    const int q = dw + 4 * m;
     if (q < KI) {
       const int i = q * 64 + lane, r = i / 17, ch = i % 17;
       dma_off[m] = r * (HD * 2) + (ch < 16 ? ch : 0) * 16;
@@ -456,17 +463,21 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
   }
   const char* kbytes = reinterpret_cast<const char*>(kp);
   const char* vbytes = reinterpret_cast<const char*>(vp);
-  auto dma = [&](const char* src, char* dst) {
+  // DMA instruction m of this wave for K block kb -> ring slot ks and V^T
+  // block vb -> slot vs. Branch free: the K/V^T choice is a select on
+  // wave-uniform values; only a wave's last instruction can be absent.
+  auto dma_one = [&](int m, int kb, int ks, int vb, int vs) {
+    const int q = dw + 4 * m;
+    if (m == NIW - 1 && NI % 4 != 0 && q >= NI) return;
+    const bool isk = q < KI;
+    const char* src = (isk ? kbytes + (size_t)kb * (BN * HD * 2) : vbytes + (size_t)vb * (BN * 2)) +
+                      dma_off[m];
+    char* dst = isk ? kbase + ks * KBYTES + q * 1024 : vbase + vs * VBYTES + (q - KI) * 1024;
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
   };
-  // Load K block kb into ring slot ks and V^T block vb into slot vs.
   auto issue = [&](int kb, int ks, int vb, int vs) {
 #pragma unroll
-    for (int m = 0; m < NIW; ++m) {
-      const int q = wave_u + 8 * m;
-      if (q < KI) dma(kbytes + (size_t)kb * BN * (HD * 2) + dma_off[m], kbase + ks * KBYTES + q * 1024);
-      else if (q < NI) dma(vbytes + (size_t)vb * (BN * 2) + dma_off[m], vbase + vs * VBYTES + (q - KI) * 1024);
-    }
+    for (int m = 0; m < NIW; ++m) dma_one(m, kb, ks, vb, vs);
   };
   // Wait until at most n of this wave's DMA loads are outstanding.
   auto wait_dma = [&](int n) {
@@ -495,6 +506,9 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
     __builtin_amdgcn_sched_barrier(0);
   };
   static_assert((NS - 2) * NIW <= 18 && NS >= 2, "wait_dma covers at most 18 loads");
+  // MFMA index after which DMA instruction m is issued inside an MFMA step.
+  constexpr int DSTEP = (2 * NQK - 8) / NIW > 0 ? (2 * NQK - 8) / NIW : 1;
+  static_assert(1 + DSTEP * (NIW - 1) < 2 * NQK, "every DMA instruction finds an MFMA slot");
 
   f32x16 acc[4];
   h2 acc16[4][8];
@@ -520,7 +534,8 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
 
   // MFMA step for block j: S^T(j) = K(j) Q^T and O^T += V^T(j-1) P^T(j-1),
   // QK and PV MFMAs interleaved, operands prefetched PF MFMAs ahead.
-  auto mfma_step = [&](const char* kb, const char* vb) {
+  auto mfma_step = [&](const char* kb, const char* vb, bool with_dma, int dkb, int dks, int dvb,
+                       int dvs) {
     // QK op n covers S tile n % KT at k-step n / KT, so consecutive QK ops
     // alternate accumulators; with PV ops in between, no accumulator is
     // reused within four MFMAs and dependent MFMAs never wait on each other.
@@ -533,12 +548,6 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
       const int dt = n % 4, ks = n / 4;
       return *reinterpret_cast<const h8*>(vb + v_lane + dt * 32 * VROW + ks * 32);
     };
-#pragma unroll
-    for (int t = 0; t < KT; ++t) s[t] = f32x16{};
-    if constexpr (ACC16) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) part[dt] = f32x16{};
-    }
     h8 fr[PF];
 #pragma unroll
     for (int i = 0; i < PF; ++i) fr[i] = ld(i);
@@ -546,14 +555,20 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
     for (int i = 0; i < 2 * NQK; ++i) {
       const h8 a = fr[i % PF];
       const int n = i >> 1;
+      // The first product into each S tile (and, for the FP16 accumulator,
+      // each PV partial) starts from a zero accumulator operand instead of
+      // zeroed registers.
       if ((i & 1) == 0) {
-        s[n % KT] = mfma32(a, qf[n / KT], s[n % KT]);
+        s[n % KT] = mfma32(a, qf[n / KT], n < KT ? f32x16{} : s[n % KT]);
       } else if constexpr (ACC16) {
-        part[n % 4] = mfma32(a, p[n / 4], part[n % 4]);
+        part[n % 4] = mfma32(a, p[n / 4], n < 4 ? f32x16{} : part[n % 4]);
       } else {
         acc[n % 4] = mfma32(a, p[n / 4], acc[n % 4]);
       }
       if (i + PF < 2 * NQK) fr[i % PF] = ld(i + PF);
+      if (i >= 1 && (i - 1) % DSTEP == 0 && (i - 1) / DSTEP < NIW) {
+        if (with_dma) dma_one((i - 1) / DSTEP, dkb, dks, dvb, dvs);
+      }
       // Keep source order: operand reads stay PF MFMAs ahead of their use.
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -566,13 +581,16 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
 
   const int nblk = seq_k / BN;
   const int last = nblk - 1;
-  // Prologue: K(0..NS-2) -> slots 0..NS-2 and V(0..NS-3) -> slots 0..NS-3,
-  // everything pairs before pair 0 would have loaded. Block indices past the
-  // end are clamped, so every pair issues the same loads and the fixed wait
-  // counts stay exact. (issue() always loads one K and one V^T block; the
-  // prologue's extra V^T loads target slots that are rewritten before use.)
+  // Prologue (group 0): K(0..NS-2) -> slots 0..NS-2 and V(0..NS-3) -> slots
+  // 0..NS-3, everything pairs before pair 0 would have loaded. Block indices
+  // past the end are clamped, so every pair issues the same loads and the
+  // fixed wait counts stay exact. (issue() always loads one K and one V^T
+  // block; the prologue's extra V^T loads target slots that are rewritten
+  // before use.)
+  if (grp == 0) {
 #pragma unroll
-  for (int i = 0; i + 1 < NS; ++i) issue(min(i, last), i, min(i, last), i);
+    for (int i = 0; i + 1 < NS; ++i) issue(min(i, last), i, min(i, last), i);
+  }
   wait_dma(0);
   lds_barrier();
 
@@ -590,16 +608,28 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
           acc16[dt][i] = acc16[dt][i] * a2 + pv;
         }
     }
-    float mx = s[0][0];
+    // Row max as a balanced 3-ary tree of v_maximum3 (independent maxima
+    // issue back to back; a running max would be one long dependent chain).
+    float mv[KT * 16];
 #pragma unroll
     for (int t = 0; t < KT; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-    mx = half_max(mx);
+      for (int r = 0; r < 16; ++r) mv[16 * t + r] = s[t][r];
+#pragma unroll
+    for (int n = KT * 16; n > 1; n = (n + 2) / 3) {
+#pragma unroll
+      for (int i = 0; 3 * i < n; ++i) {
+        float x = mv[3 * i];
+        if (3 * i + 1 < n) x = smax(x, mv[3 * i + 1]);
+        if (3 * i + 2 < n) x = smax(x, mv[3 * i + 2]);
+        mv[i] = x;
+      }
+    }
+    const float mx = half_max(mv[0]);
     const bool need = (mx - m) * c > TAU;
     float alpha = 1.f;
     if (__builtin_amdgcn_ballot_w64(need)) {
-      const float mnew = need ? fmaxf(m, mx) : m;
+      const float mnew = need ? smax(m, mx) : m;
       alpha = __builtin_amdgcn_exp2f((m - mnew) * c);
       m = mnew;
       lsum *= alpha;
@@ -610,7 +640,8 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
     }
     alpha_prev = alpha;
     const float mc = m * c;
-    float ls = 0.f;
+    // Row sum of the rounded P in four independent partial sums.
+    float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
 #pragma unroll
@@ -623,55 +654,49 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
           const h2 pr = {(_Float16)p0, (_Float16)p1};
           frag[e] = pr[0];
           frag[e + 1] = pr[1];
-          ls = __builtin_amdgcn_fdot2(pr, ones, ls, false);
+          ls[e >> 1] = __builtin_amdgcn_fdot2(pr, ones, ls[e >> 1], false);
         }
         p[2 * t + g2] = frag;
       }
     }
-    lsum += ls;
+    lsum += (ls[0] + ls[1]) + (ls[2] + ls[3]);
   };
   auto next = [](int sl) { return sl == NS - 1 ? 0 : sl + 1; };
   auto prev = [](int sl) { return sl == 0 ? NS - 1 : sl - 1; };
-  // Phase pair t (slot_t = t % NS): load K(t+NS-1) into slot (t-1) % NS and
-  // V(t+NS-2) into slot (t-2) % NS, the slots pair t-1 finished with.
-  auto issue_pair = [&](int t, int slot_t) {
-    issue(min(t + NS - 1, last), prev(slot_t), min(t + NS - 2, last), prev(prev(slot_t)));
-  };
   auto kslot = [&](int sl) { return kbase + sl * KBYTES; };
   auto vslot = [&](int sl) { return vbase + sl * VBYTES; };
   const int keep = (NS - 2) * n_dma;     // loads of later pairs still in flight
 
   // Phase 2j + grp is this wave's MFMA step for block j, phase 2j + grp + 1
   // its VALU step; both groups pass the same 2 * nblk + 2 barriers. sl is
-  // j % NS, the ring slot of K(j); V(j-1) sits in slot (j - 1) % NS.
+  // j % NS, the ring slot of K(j); V(j-1) sits in slot (j - 1) % NS. Pair j
+  // loads K(j+NS-1) into slot (j-1) % NS and V(j+NS-2) into slot (j-2) % NS,
+  // the slots pair j-1 finished with.
   int sl = 0;
   if (grp == 0) {
     for (int j = 0; j < nblk; ++j) {
-      issue_pair(j, sl);             // phase 2j: pair j starts
-      mfma_step(kslot(sl), vslot(prev(sl)));
+      const int sp = prev(sl);
+      mfma_step(kslot(sl), vslot(sp), true, min(j + NS - 1, last), sp, min(j + NS - 2, last),
+                prev(sp));             // phase 2j: pair j starts
       lds_barrier();
       valu_step();                   // phase 2j + 1
       wait_dma(keep);                // K(j+1), V(j) have landed
       lds_barrier();
       sl = next(sl);
     }
-    mfma_step(kslot(sl), vslot(prev(sl)));   // phase 2 nblk: PV(nblk - 1)
+    mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0);   // phase 2 nblk: PV(nblk - 1)
     lds_barrier();
     lds_barrier();                           // phase 2 nblk + 1: idle
   } else {
-    issue_pair(0, 0);                // phase 0: pair 0 starts; this group idles
-    lds_barrier();
+    lds_barrier();                   // phase 0: this group idles
     for (int j = 0; j < nblk; ++j) {
-      mfma_step(kslot(sl), vslot(prev(sl)));   // phase 2j + 1
-      wait_dma(keep);                // K(j+1), V(j) have landed
+      mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0);   // phase 2j + 1
       lds_barrier();
-      const int sn = next(sl);
-      issue_pair(j + 1, sn);         // phase 2j + 2: pair j + 1 starts
-      valu_step();
+      valu_step();                   // phase 2j + 2
       lds_barrier();
-      sl = sn;
+      sl = next(sl);
     }
-    mfma_step(kslot(sl), vslot(prev(sl)));   // phase 2 nblk + 1: PV(nblk - 1)
+    mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0);   // phase 2 nblk + 1: PV(nblk - 1)
     lds_barrier();
   }
   // No DMA may still be writing this workgroup's LDS when it exits.
@@ -845,6 +870,15 @@ int fa_fwd_tile(const fa_problem* p, int32_t* rows, int32_t* keys) {
   if (rc) return rc;
   *rows = tile->rows;
   *keys = tile->keys;
+  return FA_OK;
+}
+
+int fa_fwd_select(const fa_problem* p, int32_t* kernel) {
+  if (!p || !kernel) return FA_ERR_NULL;
+  const TileConfig* tile = nullptr;
+  int rc = select_tile(p, &tile);
+  if (rc) return rc;
+  *kernel = (int32_t)(tile - kTiles) + 1;
   return FA_OK;
 }
 

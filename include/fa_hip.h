@@ -87,6 +87,14 @@ int fa_fwd(const fa_problem* p, const void* q, const void* k, const void* v, voi
  */
 int fa_fwd_tile(const fa_problem* p, int32_t* rows, int32_t* keys);
 
+/*
+ * Tile configuration (1..fa_kernel_count()) fa_fwd() would launch for *p,
+ * with p->kernel == 0 resolved to the automatic choice. Lets a caller name
+ * the kernel it timed, as the reference's profiler identifies a backend's
+ * device kernel by name (core/profiler.py:14-25).
+ */
+int fa_fwd_select(const fa_problem* p, int32_t* kernel);
+
 /* Number of selectable tile configurations (valid fa_problem.kernel values are 1..n). */
 int fa_kernel_count(void);
 

@@ -91,6 +91,26 @@ def test_kernel_table(lib):
         rows, keys = C.c_int32(), C.c_int32()
         assert lib.fa_fwd_tile(C.byref(problem(kernel=i)), C.byref(rows), C.byref(keys)) == 0
         assert rows.value % 32 == 0 and keys.value % 32 == 0
+        sel = C.c_int32()
+        assert lib.fa_fwd_select(C.byref(problem(kernel=i)), C.byref(sel)) == 0
+        assert (sel.value == i) if i else (1 <= sel.value <= n)
+    sel = C.c_int32()
+    assert lib.fa_fwd_select(C.byref(problem(kernel=n + 1)), C.byref(sel)) == 9
+    assert lib.fa_fwd_select(None, C.byref(sel)) == 1
+
+
+def test_automatic_choice_fits_the_problem(lib):
+    # kernel = 0 picks a tile whose granularity divides the problem; the
+    # headline shape gets the 128-key ping-pong tile.
+    for seq in (4096, 32768, 131072, 512, 768):
+        prob = problem(seq_q=seq, seq_k=seq)
+        sel, rows, keys = C.c_int32(), C.c_int32(), C.c_int32()
+        assert lib.fa_fwd_select(C.byref(prob), C.byref(sel)) == 0
+        assert lib.fa_fwd_tile(C.byref(prob), C.byref(rows), C.byref(keys)) == 0
+        assert seq % rows.value == 0 and seq % keys.value == 0, (seq, sel.value)
+    prob = problem(batch=2, seq_q=131072, seq_k=131072)
+    assert lib.fa_fwd_select(C.byref(prob), C.byref(sel)) == 0
+    assert lib.fa_kernel_name(sel.value) == b"pp_n128_r2"
 
 
 def test_operator_validation_without_gpu(library_path):

@@ -1,0 +1,79 @@
+"""Host-side measurement helpers: rocprofv3 summaries and bench.py's traffic lookup."""
+
+import csv
+import os
+import sqlite3
+
+import pytest
+
+from fa_amd.core import kernel_stats, traffic
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+HEADER = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id", "Thread_Id",
+          "Grid_Size", "Kernel_Id", "Kernel_Name", "Workgroup_Size", "LDS_Block_Size",
+          "Scratch_Size", "VGPR_Count", "Accum_VGPR_Count", "SGPR_Count", "Counter_Name",
+          "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+
+
+def write_counters(folder, counter, rows):
+    os.makedirs(folder, exist_ok=True)
+    with open(os.path.join(folder, "run_counter_collection.csv"), "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(HEADER)
+        for dispatch, name, value in rows:
+            rec = dict.fromkeys(HEADER, "0")
+            rec.update(Dispatch_Id=str(dispatch), Kernel_Name=name, Counter_Name=counter,
+                       Counter_Value=str(value))
+            w.writerow([rec[h] for h in HEADER])
+
+
+def test_traffic_scales_by_the_calibration_kernel(tmp_path):
+    attn, copy = "hip_fa_fp32acc_kernel<1>", "elementwise bitwise_not kernel"
+    # Per-dispatch values are summed over rows (channels); the calibration
+    # kernel under-reads fetches by 2x, which the factor undoes.
+    write_counters(tmp_path / "f", "FETCH_SIZE", [
+        (1, attn, 600.0), (1, attn, 400.0), (2, attn, 1000.0), (3, copy, 512.0)])
+    write_counters(tmp_path / "w", "WRITE_SIZE", [(1, attn, 10.0), (2, attn, 10.0), (3, copy, 1024.0)])
+    s = traffic.summarize(str(tmp_path / "f"), str(tmp_path / "w"), copy_mib=1,
+                          attn_needle="hip_fa_", copy_needle="bitwise_not")
+    assert s["fetch_kib"] == 1000.0 and s["write_kib"] == 10.0
+    assert s["fetch_factor"] == pytest.approx(2.0) and s["write_factor"] == pytest.approx(1.0)
+    assert s["fetch_bytes"] == pytest.approx(2000.0 * 1024)
+    assert s["write_bytes"] == pytest.approx(10.0 * 1024)
+
+
+def test_traffic_requires_one_matching_kernel(tmp_path):
+    write_counters(tmp_path / "f", "FETCH_SIZE", [(1, "a", 1.0)])
+    write_counters(tmp_path / "w", "WRITE_SIZE", [(1, "a", 1.0)])
+    with pytest.raises(ValueError):
+        traffic.summarize(str(tmp_path / "f"), str(tmp_path / "w"), copy_mib=1)
+
+
+def test_kernel_stats_from_rocpd_db(tmp_path):
+    db = tmp_path / "out" / "run_results.db"
+    db.parent.mkdir()
+    con = sqlite3.connect(db)
+    con.execute("CREATE TABLE kernels (name TEXT, duration INTEGER)")
+    con.executemany("INSERT INTO kernels VALUES (?, ?)",
+                    [("hip_fa_fp32acc_kernel", 100), ("hip_fa_fp32acc_kernel", 300), ("fa_vt", 10)])
+    con.commit()
+    con.close()
+    stats = kernel_stats.collect(str(tmp_path / "out"))
+    assert stats == {"hip_fa_fp32acc_kernel": [100.0, 300.0], "fa_vt": [10.0]}
+    text = kernel_stats.render(stats, flops=2e9, match="hip_fa_fp32acc")
+    # 2e9 FLOP / 200 ns average = 1e16 FLOP/s = 10000 TFLOP/s
+    assert "10000.0 TFLOP/s" in text
+    assert text.splitlines()[1].startswith("hip_fa_fp32acc_kernel")
+
+
+def test_bench_reads_the_committed_traffic_summary():
+    import bench
+
+    key = "hip_fa_fp32acc c3 B2_S131072_Q12_KV1_D128 tile=pp_n128_r2"
+    path = os.path.join(REPO, "profiles", "hip_fa_fp32acc_c3_traffic.txt")
+    if not os.path.exists(path):
+        pytest.skip("no traffic summary committed")
+    value = bench.traffic_from_profiles(key)
+    assert isinstance(value, int) and value > 1_677_721_600   # at least the algorithmic bytes
+    assert bench.traffic_from_profiles(key + "x") is None

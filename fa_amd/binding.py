@@ -5,7 +5,8 @@ Mirrors the reference's operator binding
 
   * the library is opened with ``RTLD_LOCAL``;
   * a call is two-phase: ``fa_fwd_workspace_bytes`` sizes the workspace,
-    ``fa_fwd`` enqueues the forward on the current torch stream;
+    ``fa_fwd`` (or ``fa_fwd_lse`` when the per-row log-sum-exp is asked for)
+    enqueues the forward on the current torch stream;
   * geometry, dtype, device and layout errors raise ``ValueError`` before any
     launch; a nonzero library status raises ``RuntimeError("fa_fwd <where>:
     <status> (<message>)")``;
@@ -44,6 +45,8 @@ SIGNATURES = {
     "fa_fwd_workspace_bytes": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_uint64)]),
     "fa_fwd": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                          C.c_void_p, C.c_uint64, C.c_void_p]),
+    "fa_fwd_lse": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                             C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
     "fa_fwd_tile": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "fa_fwd_select": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32)]),
     "fa_kernel_count": (C.c_int, []),
@@ -132,15 +135,20 @@ class Operator:
                     or not t.is_contiguous():
                 raise ValueError("Q/K/V must be contiguous FP16 on the same GPU")
 
-    def buffers_for(self, q, k):
+    def buffers_for(self, q, k, lse=False):
         import torch
 
-        key = (tuple(q.shape), tuple(k.shape), q.device, self.config)
+        key = (tuple(q.shape), tuple(k.shape), q.device, self.config, lse)
         if key not in self.buffers:
-            self.buffers[key] = torch.empty(q.shape, dtype=torch.float16, device=q.device)
+            if lse:
+                self.buffers[key] = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
+            else:
+                self.buffers[key] = torch.empty(q.shape, dtype=torch.float16, device=q.device)
         return self.buffers[key]
 
-    def __call__(self, q, k, v, scale=None):
+    def __call__(self, q, k, v, scale=None, return_lse=False):
+        """O (cached tensor), or (O, lse) with ``return_lse``: lse [B, Hq, Nq] FP32
+        natural-log log-sum-exp of the scaled scores of each query row."""
         import torch
 
         self.validate(q, k, v)
@@ -151,16 +159,21 @@ class Operator:
         size = C.c_uint64()
         self.check(self.lib.fa_fwd_workspace_bytes(C.byref(prob), C.byref(size)), "prepare")
         out = self.buffers_for(q, k)
+        lse = self.buffers_for(q, k, lse=True) if return_lse else None
         with torch.cuda.device(q.device):
             need = max(size.value, 16)
             if self.workspace is None or self.workspace.device != q.device \
                     or self.workspace.numel() < need:
                 self.workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
             stream = torch.cuda.current_stream(q.device)
-            self.check(self.lib.fa_fwd(C.byref(prob), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                       out.data_ptr(), self.workspace.data_ptr(),
-                                       self.workspace.numel(), C.c_void_p(stream.cuda_stream)),
-                       "launch")
-            for t in (q, k, v, out, self.workspace):
+            common = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
+            tail = (self.workspace.data_ptr(), self.workspace.numel(),
+                    C.c_void_p(stream.cuda_stream))
+            if return_lse:
+                status = self.lib.fa_fwd_lse(C.byref(prob), *common, lse.data_ptr(), *tail)
+            else:
+                status = self.lib.fa_fwd(C.byref(prob), *common, *tail)
+            self.check(status, "launch")
+            for t in (q, k, v, out, self.workspace) + ((lse,) if return_lse else ()):
                 t.record_stream(stream)
-        return out
+        return (out, lse) if return_lse else out

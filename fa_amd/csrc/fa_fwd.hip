@@ -53,6 +53,22 @@ constexpr int HD = 128;               // head dimension
 constexpr int VT_GROUP = 64;          // keys per V-transpose workgroup
 constexpr float NEG_BIG = -1.0e30f;   // finite "minus infinity" for the running max
 constexpr double LOG2E = 1.4426950408889634;
+constexpr float LN2 = 0.6931471805599453f;
+
+// Kernel arguments. seq_k is the key length of the K and V^T buffers the
+// kernel reads (a multiple of its key block); keys at or past nk_valid are
+// zero padding and masked out of the softmax. lse (FP32 [B, Hq, Nq],
+// natural-log log-sum-exp of the scaled scores) may be null. c is the softmax
+// scale times log2(e).
+struct FaArgs {
+  const _Float16* q;
+  const _Float16* k;
+  const _Float16* vt;
+  _Float16* o;
+  float* lse;
+  int heads_q, group, seq_q, seq_k, nk_valid;
+  float c;
+};
 
 // 16-byte chunk swizzle for an LDS tile whose rows are CPR chunks long.
 // Rows are read 32 at a time at one logical chunk column; the XOR spreads any
@@ -89,23 +105,36 @@ __device__ __forceinline__ int vt_key_of_slot(int slot) {
 }
 
 // vt[kv][d][key0 + slot] = v[kv][key0 + key(slot)][d], one 64-key group per
-// workgroup. Grid (Nk / 64, B * Hkv), 256 threads.
-__global__ void __launch_bounds__(256) fa_vt_kernel(const _Float16* __restrict__ v,
-                                                    _Float16* __restrict__ vt, int seq_k) {
+// workgroup; keys at or past nk_valid become zeros. With kpad non-null the
+// group's K rows are also copied to kpad[kv][key0 + r] (zero rows past
+// nk_valid), the padded K a masked key tail reads. Grid (nk_pad / 64, B * Hkv),
+// 256 threads; v and k hold nk_valid keys per head, vt and kpad nk_pad.
+__global__ void __launch_bounds__(256) fa_prep_kernel(const _Float16* __restrict__ k,
+                                                      const _Float16* __restrict__ v,
+                                                      _Float16* __restrict__ vt,
+                                                      _Float16* __restrict__ kpad, int nk_valid,
+                                                      int nk_pad) {
   __shared__ _Float16 tile[VT_GROUP][HD + 8];
   const int tid = threadIdx.x;
   const size_t kv = blockIdx.y;
   const int key0 = blockIdx.x * VT_GROUP;
-  const _Float16* src = v + (kv * seq_k + key0) * HD;
+  const _Float16* src = v + (kv * nk_valid + key0) * HD;
+  const _Float16* ksrc = k + (kv * nk_valid + key0) * HD;
+  _Float16* kdst = kpad ? kpad + (kv * nk_pad + key0) * HD : nullptr;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int i = tid + 256 * j;
     const int r = i >> 4, ch = i & 15;
+    const bool valid = key0 + r < nk_valid;
+    const u32x4 zero = {0u, 0u, 0u, 0u};
     *reinterpret_cast<u32x4*>(&tile[r][ch * 8]) =
-        *reinterpret_cast<const u32x4*>(src + (size_t)r * HD + ch * 8);
+        valid ? *reinterpret_cast<const u32x4*>(src + (size_t)r * HD + ch * 8) : zero;
+    if (kdst)
+      *reinterpret_cast<u32x4*>(kdst + (size_t)r * HD + ch * 8) =
+          valid ? *reinterpret_cast<const u32x4*>(ksrc + (size_t)r * HD + ch * 8) : zero;
   }
   __syncthreads();
-  _Float16* dst = vt + kv * HD * (size_t)seq_k + key0;
+  _Float16* dst = vt + kv * HD * (size_t)nk_pad + key0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int i = tid + 256 * j;
@@ -116,18 +145,21 @@ __global__ void __launch_bounds__(256) fa_vt_kernel(const _Float16* __restrict__
       const int slot = (ch & 1) * 8 + e;
       val[e] = tile[16 * (ch >> 1) + vt_key_of_slot(slot)][d];
     }
-    *reinterpret_cast<h8*>(dst + (size_t)d * seq_k + ch * 8) = val;
+    *reinterpret_cast<h8*>(dst + (size_t)d * nk_pad + ch * 8) = val;
   }
 }
 
 // The attention body. ACC16 selects the FP16 O accumulator; NW waves per
 // workgroup, SUB 32-row subtiles per wave, BN keys per block.
+// Requires Nq % BM == 0 and Nk % BN == 0 (no masked tail).
 template <bool ACC16, int NW, int SUB, int BN>
-__device__ __forceinline__ void fa_fwd_body(const _Float16* __restrict__ q,
-                                            const _Float16* __restrict__ k,
-                                            const _Float16* __restrict__ vt,
-                                            _Float16* __restrict__ o, int heads_q, int group,
-                                            int seq_q, int seq_k, float c) {
+__device__ __forceinline__ void fa_fwd_body(const FaArgs& args) {
+  const _Float16* __restrict__ q = args.q;
+  const _Float16* __restrict__ k = args.k;
+  const _Float16* __restrict__ vt = args.vt;
+  _Float16* __restrict__ o = args.o;
+  const int heads_q = args.heads_q, group = args.group, seq_q = args.seq_q, seq_k = args.seq_k;
+  const float c = args.c;
   constexpr int NT = NW * 64;
   constexpr int BM = NW * SUB * 32;
   constexpr int KT = BN / 32;          // 32-key S^T tiles per block
@@ -327,10 +359,14 @@ __device__ __forceinline__ void fa_fwd_body(const _Float16* __restrict__ q,
     __syncthreads();
   }
 
-  // Epilogue: O / l -> FP16. Lane holds dims 32dt + 8g + 4hf + (0..3).
+  // Epilogue: O / l -> FP16 (lane holds dims 32dt + 8g + 4hf + (0..3)), and
+  // the row's log-sum-exp ln(l) + scale * m = (log2(l) + c * m) * ln 2.
 #pragma unroll
   for (int u = 0; u < SUB; ++u) {
-    const float inv = 1.f / half_sum(lsum[u]);
+    const float l = half_sum(lsum[u]);
+    const float inv = 1.f / l;
+    if (args.lse && hf == 0)
+      args.lse[row0 + u * 32 + l32] = (__builtin_amdgcn_logf(l) + m[u] * c) * LN2;
     _Float16* orow = op + (size_t)(u * 32 + l32) * HD;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
@@ -384,11 +420,14 @@ __device__ __forceinline__ void lds_barrier() {
 // rescale runs only on the rare blocks where some row of the wave needs it.
 // With TAU = 0 the max tracks every increase (FP16 O must not grow).
 template <bool ACC16, int BN, int NS, bool SPLIT_HI>
-__device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
-                                           const _Float16* __restrict__ k,
-                                           const _Float16* __restrict__ vt,
-                                           _Float16* __restrict__ o, int heads_q, int group,
-                                           int seq_q, int seq_k, float c) {
+__device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
+  const _Float16* __restrict__ q = args.q;
+  const _Float16* __restrict__ k = args.k;
+  const _Float16* __restrict__ vt = args.vt;
+  _Float16* __restrict__ o = args.o;
+  const int heads_q = args.heads_q, group = args.group, seq_q = args.seq_q, seq_k = args.seq_k;
+  const int nk_valid = args.nk_valid;
+  const float c = args.c;
   constexpr int NT = 512;
   constexpr int BM = 256;
   constexpr int KT = BN / 32;            // 32-key S^T tiles per block
@@ -427,7 +466,9 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
   // 2s+1 under paired placement.
   const int grp = SPLIT_HI ? (wave_u >> 2) : (wave_u & 1);
 
-  const int tiles_q = seq_q / BM;
+  // Query tiles may run past Nq (a ragged last tile): its rows past the end
+  // compute on a copy of the last row and store nothing.
+  const int tiles_q = (seq_q + BM - 1) / BM;
   const int bh = blockIdx.x / tiles_q;
   const int qt = blockIdx.x - bh * tiles_q;
   const int b = bh / heads_q, h = bh - b * heads_q;
@@ -435,14 +476,14 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
   const size_t kv = (size_t)b * heads_kv + h / group;
   const _Float16* kp = k + kv * (size_t)seq_k * HD;
   const _Float16* vp = vt + kv * (size_t)HD * seq_k;
-  const size_t row0 = (size_t)bh * seq_q + (size_t)qt * BM + (size_t)wave_u * 32;
-  const _Float16* qp = q + row0 * HD;
-  _Float16* op = o + row0 * HD;
+  const int row = qt * BM + wave_u * 32 + l32;          // this lane's query row in (b, h)
+  const bool row_ok = row < seq_q;
+  const size_t grow = (size_t)bh * seq_q + (row_ok ? row : seq_q - 1);
 
   h8 qf[8];
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk)
-    qf[kk] = *reinterpret_cast<const h8*>(qp + (size_t)l32 * HD + kk * 16 + hf * 8);
+    qf[kk] = *reinterpret_cast<const h8*>(q + grow * HD + kk * 16 + hf * 8);
 
   // Group-0 wave dw issues DMA instructions q = dw + 4m (m < NIW, q < NI);
   // q < KI is K instruction q, otherwise V^T instruction q - KI. The per-lane
@@ -596,7 +637,7 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
 
   // VALU step: online softmax of S(j) into P(j) (and, for the FP16
   // accumulator, the merge of the PV(j-1) partial computed by MFMA step j).
-  auto valu_step = [&]() {
+  auto valu_step = [&](int key0) {
     if constexpr (ACC16) {
       const _Float16 a16 = (_Float16)alpha_prev;
       const h2 a2 = {a16, a16};
@@ -607,6 +648,16 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
           const h2 pv = {(_Float16)part[dt][2 * i], (_Float16)part[dt][2 * i + 1]};
           acc16[dt][i] = acc16[dt][i] * a2 + pv;
         }
+    }
+    // Keys at or past nk_valid (zero padding of a ragged last block) score
+    // -inf: they get P = 0. S^T register r of lane half hf holds key
+    // 32t + 8(r / 4) + 4hf + r % 4 of the block.
+    if (key0 + BN > nk_valid) {
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (key0 + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3) >= nk_valid) s[t][r] = -INFINITY;
     }
     // Row max as a balanced 3-ary tree of v_maximum3 (independent maxima
     // issue back to back; a running max would be one long dependent chain).
@@ -679,7 +730,7 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
       mfma_step(kslot(sl), vslot(sp), true, min(j + NS - 1, last), sp, min(j + NS - 2, last),
                 prev(sp));             // phase 2j: pair j starts
       lds_barrier();
-      valu_step();                   // phase 2j + 1
+      valu_step(j * BN);             // phase 2j + 1
       wait_dma(keep);                // K(j+1), V(j) have landed
       lds_barrier();
       sl = next(sl);
@@ -692,7 +743,7 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
     for (int j = 0; j < nblk; ++j) {
       mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0);   // phase 2j + 1
       lds_barrier();
-      valu_step();                   // phase 2j + 2
+      valu_step(j * BN);             // phase 2j + 2
       lds_barrier();
       sl = next(sl);
     }
@@ -715,8 +766,13 @@ __device__ __forceinline__ void fa_pp_body(const _Float16* __restrict__ q,
       }
   }
 
-  const float inv = 1.f / half_sum(lsum);
-  _Float16* orow = op + (size_t)l32 * HD;
+  // Epilogue: O / l -> FP16 and the row's log-sum-exp
+  // ln(l) + scale * m = (log2(l) + c * m) * ln 2, for rows inside Nq.
+  const float l = half_sum(lsum);
+  const float inv = 1.f / l;
+  if (!row_ok) return;
+  if (args.lse && hf == 0) args.lse[grow] = (__builtin_amdgcn_logf(l) + m * c) * LN2;
+  _Float16* orow = o + grow * HD;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
@@ -744,11 +800,9 @@ template <int KIND, int P1>
 constexpr int kThreads = KIND ? 512 : P1 * 64;
 
 template <bool ACC16, int KIND, int P1, int P2, int BN>
-__device__ __forceinline__ void fa_dispatch(const _Float16* q, const _Float16* k,
-                                            const _Float16* vt, _Float16* o, int heads_q,
-                                            int group, int seq_q, int seq_k, float c) {
-  if constexpr (KIND == 0) fa_fwd_body<ACC16, P1, P2, BN>(q, k, vt, o, heads_q, group, seq_q, seq_k, c);
-  else fa_pp_body<ACC16, BN, P1, P2 == 1>(q, k, vt, o, heads_q, group, seq_q, seq_k, c);
+__device__ __forceinline__ void fa_dispatch(const FaArgs& args) {
+  if constexpr (KIND == 0) fa_fwd_body<ACC16, P1, P2, BN>(args);
+  else fa_pp_body<ACC16, BN, P1, P2 == 1>(args);
 }
 
 // Device entry points, one per accumulation variant. Their names contain the
@@ -756,25 +810,20 @@ __device__ __forceinline__ void fa_dispatch(const _Float16* q, const _Float16* k
 // attributes kernel time (WPE = waves per SIMD the register budget targets).
 template <int KIND, int P1, int P2, int BN, int WPE>
 __global__ void __launch_bounds__((kThreads<KIND, P1>)) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-hip_fa_fp32acc_kernel(const _Float16* __restrict__ q, const _Float16* __restrict__ k,
-                      const _Float16* __restrict__ vt, _Float16* __restrict__ o, int heads_q,
-                      int group, int seq_q, int seq_k, float c) {
-  fa_dispatch<false, KIND, P1, P2, BN>(q, k, vt, o, heads_q, group, seq_q, seq_k, c);
+hip_fa_fp32acc_kernel(FaArgs args) {
+  fa_dispatch<false, KIND, P1, P2, BN>(args);
 }
 
 template <int KIND, int P1, int P2, int BN, int WPE>
 __global__ void __launch_bounds__((kThreads<KIND, P1>)) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-hip_fa_fp16acc_kernel(const _Float16* __restrict__ q, const _Float16* __restrict__ k,
-                      const _Float16* __restrict__ vt, _Float16* __restrict__ o, int heads_q,
-                      int group, int seq_q, int seq_k, float c) {
-  fa_dispatch<true, KIND, P1, P2, BN>(q, k, vt, o, heads_q, group, seq_q, seq_k, c);
+hip_fa_fp16acc_kernel(FaArgs args) {
+  fa_dispatch<true, KIND, P1, P2, BN>(args);
 }
 
 // ----------------------------------------------------------------------------
 // Host side: tile table, validation, launch.
 
-typedef void (*attn_fn)(const _Float16*, const _Float16*, const _Float16*, _Float16*, int, int,
-                        int, int, float);
+typedef void (*attn_fn)(FaArgs);
 
 struct TileConfig {
   const char* name;
@@ -782,6 +831,7 @@ struct TileConfig {
   int rows;        // BM
   int keys;        // BN
   int lds;         // dynamic LDS bytes per workgroup
+  bool tails;      // masks ragged query and key tails (any Nq, Nk)
   attn_fn fp32;
   attn_fn fp16;
 };
@@ -789,7 +839,8 @@ struct TileConfig {
 #define FA_TILE(NAME, KIND, P1, P2, BN, WPE)                                                 \
   TileConfig {                                                                             \
     NAME, kThreads<KIND, P1>, (KIND ? 8 : P1 * P2) * 32, BN,                               \
-        (KIND ? pp_lds_bytes(BN, P1) : 0), &hip_fa_fp32acc_kernel<KIND, P1, P2, BN, WPE>,   \
+        (KIND ? pp_lds_bytes(BN, P1) : 0), KIND == 1,                                      \
+        &hip_fa_fp32acc_kernel<KIND, P1, P2, BN, WPE>,                                     \
         &hip_fa_fp16acc_kernel<KIND, P1, P2, BN, WPE>                                      \
   }
 
@@ -802,18 +853,28 @@ const TileConfig kTiles[] = {
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 // Automatic choice (fa_problem.kernel == 0): the first of these 1-based tile
-// indices, fastest first, whose query-row and key granularity divide the
-// problem; the first entry when none does (validation then reports the tail).
-constexpr int kAutoOrder[] = {5, 3, 2, 1};
+// indices, fastest first (measured at N = 32768), that fits the problem (masks
+// tails, or its query-row and key granularity divide Nq and Nk). The FP16
+// accumulator's 128-key tile spills registers, so that variant prefers the
+// 64-key ring.
+constexpr int kAutoOrderFp32[] = {5, 4, 3, 2, 1};
+constexpr int kAutoOrderFp16[] = {4, 3, 5, 2, 1};
+static_assert(sizeof(kAutoOrderFp32) == sizeof(int) * kNumTiles &&
+                  sizeof(kAutoOrderFp16) == sizeof(int) * kNumTiles,
+              "every tile appears in each automatic order");
+
+bool tile_fits(const TileConfig& t, const fa_problem* p) {
+  return t.tails || (p->seq_q > 0 && p->seq_k > 0 && p->seq_q % t.rows == 0 && p->seq_k % t.keys == 0);
+}
 
 int select_tile(const fa_problem* p, const TileConfig** out) {
   int idx = p->kernel;
   if (idx == 0) {
-    idx = kAutoOrder[0];
-    for (int cand : kAutoOrder) {
-      const TileConfig& t = kTiles[cand - 1];
-      if (p->seq_q > 0 && p->seq_k > 0 && p->seq_q % t.rows == 0 && p->seq_k % t.keys == 0) {
-        idx = cand;
+    const int* order = p->acc == FA_ACC_FP16 ? kAutoOrderFp16 : kAutoOrderFp32;
+    idx = order[0];
+    for (int n = 0; n < kNumTiles; ++n) {
+      if (tile_fits(kTiles[order[n] - 1], p)) {
+        idx = order[n];
         break;
       }
     }
@@ -821,6 +882,27 @@ int select_tile(const fa_problem* p, const TileConfig** out) {
   if (idx < 1 || idx > kNumTiles) return FA_ERR_KERNEL;
   *out = &kTiles[idx - 1];
   return FA_OK;
+}
+
+// Key length of the K and V^T buffers the attention kernel reads: Nk itself
+// when the tile's key block divides it, else Nk rounded up to a whole block
+// (64 or 128 keys, both multiples of the transpose group), zero-padded by the
+// prep kernel, with the padded K copied into the workspace too. The last
+// block then holds at least one real key.
+struct KeyLayout {
+  int64_t nk_pad;
+  bool pad_k;
+  uint64_t vt_bytes, k_bytes;
+};
+
+KeyLayout key_layout(const fa_problem* p, const TileConfig* tile) {
+  KeyLayout lay;
+  lay.pad_k = p->seq_k % tile->keys != 0;
+  lay.nk_pad = lay.pad_k ? (p->seq_k + tile->keys - 1) / tile->keys * tile->keys : p->seq_k;
+  static_assert(VT_GROUP == 64, "key blocks of 64 and 128 are whole transpose groups");
+  lay.vt_bytes = (uint64_t)p->batch * p->heads_kv * lay.nk_pad * HD * sizeof(_Float16);
+  lay.k_bytes = lay.pad_k ? lay.vt_bytes : 0;
+  return lay;
 }
 
 int validate(const fa_problem* p, const TileConfig** tile) {
@@ -835,19 +917,60 @@ int validate(const fa_problem* p, const TileConfig** tile) {
   if (p->reserved != 0) return FA_ERR_KERNEL;
   int rc = select_tile(p, tile);
   if (rc) return rc;
-  // 32-bit index limits used inside the kernels.
+  // 32-bit index limits used inside the kernels (the padded key length too).
   const int64_t lim = (int64_t)1 << 30;
-  if (p->seq_q >= lim || p->seq_k >= lim || p->heads_q >= lim || p->batch >= lim)
+  if (p->seq_q >= lim || p->seq_k >= lim - 128 || p->heads_q >= lim || p->batch >= lim)
     return FA_ERR_GEOMETRY;
   const int64_t bh = p->batch * p->heads_q;
-  if (bh >= lim || (bh * (p->seq_q / (*tile)->rows)) >= lim || p->batch * p->heads_kv >= 65536)
-    return FA_ERR_GEOMETRY;
-  if (p->seq_q % (*tile)->rows || p->seq_k % (*tile)->keys || p->seq_k % VT_GROUP) return FA_ERR_TAIL;
+  const int64_t tiles_q = (p->seq_q + (*tile)->rows - 1) / (*tile)->rows;
+  if (bh >= lim || bh * tiles_q >= lim || p->batch * p->heads_kv >= 65536) return FA_ERR_GEOMETRY;
+  if (!tile_fits(**tile, p)) return FA_ERR_TAIL;
   return FA_OK;
 }
 
-uint64_t workspace_for(const fa_problem* p) {
-  return (uint64_t)p->batch * p->heads_kv * p->seq_k * p->dim * sizeof(_Float16);
+int launch(const fa_problem* p, const void* q, const void* k, const void* v, void* o, float* lse,
+           void* workspace, uint64_t workspace_bytes, void* stream) {
+  const TileConfig* tile = nullptr;
+  int rc = validate(p, &tile);
+  if (rc) return rc;
+  if (!q || !k || !v || !o) return FA_ERR_NULL;
+  const KeyLayout lay = key_layout(p, tile);
+  if (!workspace || workspace_bytes < lay.vt_bytes + lay.k_bytes) return FA_ERR_WORKSPACE;
+  for (const void* ptr : {q, k, v, (const void*)o, (const void*)workspace, (const void*)lse})
+    if (reinterpret_cast<uintptr_t>(ptr) & 15) return FA_ERR_ALIGN;
+
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  _Float16* vt = static_cast<_Float16*>(workspace);
+  _Float16* kpad = lay.pad_k ? vt + lay.vt_bytes / sizeof(_Float16) : nullptr;
+
+  (void)hipGetLastError();  // clear any stale error so the checks below see only ours
+  dim3 prep_grid((unsigned)(lay.nk_pad / VT_GROUP), (unsigned)(p->batch * p->heads_kv));
+  hipLaunchKernelGGL(fa_prep_kernel, prep_grid, dim3(256), 0, st, static_cast<const _Float16*>(k),
+                     static_cast<const _Float16*>(v), vt, kpad, (int)p->seq_k, (int)lay.nk_pad);
+  if (hipGetLastError() != hipSuccess) return FA_ERR_LAUNCH;
+
+  FaArgs args;
+  args.q = static_cast<const _Float16*>(q);
+  args.k = lay.pad_k ? kpad : static_cast<const _Float16*>(k);
+  args.vt = vt;
+  args.o = static_cast<_Float16*>(o);
+  args.lse = lse;
+  args.heads_q = (int)p->heads_q;
+  args.group = (int)(p->heads_q / p->heads_kv);
+  args.seq_q = (int)p->seq_q;
+  args.seq_k = (int)lay.nk_pad;
+  args.nk_valid = (int)p->seq_k;
+  args.c = (float)((double)p->scale * LOG2E);
+  const int64_t tiles_q = (p->seq_q + tile->rows - 1) / tile->rows;
+  const unsigned grid = (unsigned)(p->batch * p->heads_q * tiles_q);
+  attn_fn fn = p->acc == FA_ACC_FP16 ? tile->fp16 : tile->fp32;
+  if (tile->lds > 65536 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, tile->lds) != hipSuccess)
+    return FA_ERR_LAUNCH;
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(tile->threads), tile->lds, st, args);
+  if (hipGetLastError() != hipSuccess) return FA_ERR_LAUNCH;
+  return FA_OK;
 }
 
 }  // namespace
@@ -859,7 +982,8 @@ int fa_fwd_workspace_bytes(const fa_problem* p, uint64_t* bytes) {
   const TileConfig* tile = nullptr;
   int rc = validate(p, &tile);
   if (rc) return rc;
-  *bytes = workspace_for(p);
+  const KeyLayout lay = key_layout(p, tile);
+  *bytes = lay.vt_bytes + lay.k_bytes;
   return FA_OK;
 }
 
@@ -868,8 +992,8 @@ int fa_fwd_tile(const fa_problem* p, int32_t* rows, int32_t* keys) {
   const TileConfig* tile = nullptr;
   int rc = select_tile(p, &tile);
   if (rc) return rc;
-  *rows = tile->rows;
-  *keys = tile->keys;
+  *rows = tile->tails ? 1 : tile->rows;
+  *keys = tile->tails ? 1 : tile->keys;
   return FA_OK;
 }
 
@@ -884,37 +1008,12 @@ int fa_fwd_select(const fa_problem* p, int32_t* kernel) {
 
 int fa_fwd(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
            void* workspace, uint64_t workspace_bytes, void* stream) {
-  const TileConfig* tile = nullptr;
-  int rc = validate(p, &tile);
-  if (rc) return rc;
-  if (!q || !k || !v || !o) return FA_ERR_NULL;
-  if (!workspace || workspace_bytes < workspace_for(p)) return FA_ERR_WORKSPACE;
-  for (const void* ptr : {q, k, v, (const void*)o, (const void*)workspace})
-    if (reinterpret_cast<uintptr_t>(ptr) & 15) return FA_ERR_ALIGN;
+  return launch(p, q, k, v, o, nullptr, workspace, workspace_bytes, stream);
+}
 
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int group = (int)(p->heads_q / p->heads_kv);
-  _Float16* vt = static_cast<_Float16*>(workspace);
-
-  (void)hipGetLastError();  // clear any stale error so the checks below see only ours
-  dim3 vt_grid((unsigned)(p->seq_k / VT_GROUP), (unsigned)(p->batch * p->heads_kv));
-  hipLaunchKernelGGL(fa_vt_kernel, vt_grid, dim3(256), 0, st, static_cast<const _Float16*>(v), vt,
-                     (int)p->seq_k);
-  if (hipGetLastError() != hipSuccess) return FA_ERR_LAUNCH;
-
-  const double c = (double)p->scale * LOG2E;
-  const unsigned grid = (unsigned)(p->batch * p->heads_q * (p->seq_q / tile->rows));
-  attn_fn fn = p->acc == FA_ACC_FP16 ? tile->fp16 : tile->fp32;
-  if (tile->lds > 65536 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, tile->lds) != hipSuccess)
-    return FA_ERR_LAUNCH;
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(tile->threads), tile->lds, st, static_cast<const _Float16*>(q),
-                     static_cast<const _Float16*>(k), static_cast<const _Float16*>(vt),
-                     static_cast<_Float16*>(o), (int)p->heads_q, group, (int)p->seq_q,
-                     (int)p->seq_k, (float)c);
-  if (hipGetLastError() != hipSuccess) return FA_ERR_LAUNCH;
-  return FA_OK;
+int fa_fwd_lse(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
+               float* lse, void* workspace, uint64_t workspace_bytes, void* stream) {
+  return launch(p, q, k, v, o, lse, workspace, workspace_bytes, stream);
 }
 
 int fa_kernel_count(void) { return kNumTiles; }
@@ -930,7 +1029,7 @@ const char* fa_strerror(int status) {
     case FA_ERR_NULL: return "required pointer is NULL";
     case FA_ERR_GEOMETRY: return "invalid attention geometry";
     case FA_ERR_DIM: return "head dimension must be 128";
-    case FA_ERR_TAIL: return "unsupported query/key tail: Nq or Nk not a multiple of the tile";
+    case FA_ERR_TAIL: return "unsupported query/key tail: Nq or Nk not a multiple of the selected tile, which has no masked tail";
     case FA_ERR_ALIGN: return "tensor pointer not 16-byte aligned";
     case FA_ERR_WORKSPACE: return "workspace missing or too small";
     case FA_ERR_ACC: return "unknown accumulation variant";

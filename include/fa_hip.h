@@ -5,7 +5,9 @@
  * Layout: q [B, Hq, Nq, 128], k and v [B, Hkv, Nk, 128], o [B, Hq, Nq, 128],
  * all contiguous FP16 in device memory. Output rows are the normalised
  * softmax(q k^T * scale) v with query head h reading key/value head
- * h / (Hq / Hkv).
+ * h / (Hq / Hkv). Any Nq, Nk >= 1 with the automatic tile choice (ragged
+ * query and key tails are masked); fa_fwd_lse() also returns the per-row
+ * log-sum-exp.
  *
  * Conventions (mirroring the reference's two-phase operator binding):
  *   - every entry point returns 0 on success and a nonzero FA_ERR_* code
@@ -33,7 +35,7 @@ enum fa_status {
   FA_ERR_NULL = 1,          /* a required pointer is NULL */
   FA_ERR_GEOMETRY = 2,      /* non-positive size, Hq % Hkv != 0, or overflowing sizes */
   FA_ERR_DIM = 3,           /* head dimension other than 128 */
-  FA_ERR_TAIL = 4,          /* Nq or Nk not a multiple of the selected tile */
+  FA_ERR_TAIL = 4,          /* Nq or Nk not a multiple of an explicitly selected tile without masked tails */
   FA_ERR_ALIGN = 5,         /* a tensor pointer is not 16-byte aligned */
   FA_ERR_WORKSPACE = 6,     /* workspace missing or smaller than fa_fwd_workspace_bytes() */
   FA_ERR_ACC = 7,           /* unknown accumulation variant */
@@ -62,7 +64,9 @@ typedef struct fa_problem {
 
 /*
  * Bytes of device workspace fa_fwd() needs for problem *p (the key-permuted
- * transposed copy of v). Replaces phase 1 of the reference's operator call,
+ * transposed copy of v; with a ragged key tail, zero-padded copies of k and
+ * v^T to a whole key block of the selected tile). Replaces phase 1 of the
+ * reference's operator call,
  * aclnn<Op>GetWorkspaceSize (backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/
  * binding.py:21-24,74-75), whose host tiling sizes the scratch buffer
  * (project/op_host/fa_fa_nk_nz_vector_fp32_v5_sumpack.cpp:52-87).
@@ -81,9 +85,22 @@ int fa_fwd(const fa_problem* p, const void* q, const void* k, const void* v, voi
            void* workspace, uint64_t workspace_bytes, void* stream);
 
 /*
- * Query-row and key-block granularity of the kernel fa_fwd() would use for
- * *p: Nq must be a multiple of *rows and Nk of *keys. Host-side counterpart
- * of the reference binding's alignment check (binding.py:95).
+ * fa_fwd() that also writes lse [B, Hq, Nq] FP32 (16-byte aligned, or NULL
+ * for none): lse[b][h][i] = ln sum_j exp(scale * q_i . k_j), the statistic a
+ * backward pass or a merge of key-sharded partial results needs. The
+ * reference exports no such output: its kernels keep the running max and sum
+ * of each row in workspace (K32/vector_output.h:22-38), which this output
+ * exposes in closed form.
+ */
+int fa_fwd_lse(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
+               float* lse, void* workspace, uint64_t workspace_bytes, void* stream);
+
+/*
+ * Query-row and key granularity the kernel fa_fwd() would use for *p needs:
+ * Nq must be a multiple of *rows and Nk of *keys (1 and 1 for the tiles that
+ * mask ragged tails, which the automatic choice always picks). Host-side
+ * counterpart of the reference binding's alignment check (binding.py:95),
+ * which demands Nq % 256 == 0 and Nk % 512 == 0.
  */
 int fa_fwd_tile(const fa_problem* p, int32_t* rows, int32_t* keys);
 

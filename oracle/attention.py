@@ -32,6 +32,14 @@ Functions and what pins each (tests/test_oracle.py):
                        against attention_f64 (FP32 rounding bound) and torch's
                        float32 scaled_dot_product_attention. It is also the
                        CPU baseline bench.py times.
+  lse_f64 / lse_rows_f64
+                       per-row log-sum-exp ln sum_j exp(scale q.k_j), the
+                       statistic the kernels' running max and sum encode
+                       (the reference keeps them per row in workspace,
+                       K32/vector_output.h:22-38, and exports none); pinned by
+                       closed forms (one key, identical keys), torch.logsumexp
+                       in float64, and the identity attention_f64 ==
+                       sum_j exp(scale s_j - lse) v_j.
 Every check above plants a mistake in the oracle (dropped scale, swapped GQA
 map, transposed operand) and confirms at least one check fails
 (tests/test_oracle.py::test_checks_catch_planted_mistakes).
@@ -136,6 +144,41 @@ def attention_rows_f64(q, k, v, rows, scale=None):
         res = p @ vf
         for m, (n, _, _) in enumerate(items):
             out[n] = res[m]
+    return out
+
+
+def _lse_rows(s):
+    """ln sum exp over the last axis of float64 scores, max-shifted."""
+    mx = s.max(axis=-1)
+    return mx + np.log(np.exp(s - mx[..., None]).sum(axis=-1))
+
+
+def lse_f64(q, k, scale=None, chunk_rows=1024):
+    """float64 [B, Hq, Nq]: lse[b,h,i] = ln sum_j exp(scale * q[b,h,i] . k[b,h//g,j])."""
+    q, k = _np(q), _np(k)
+    b_, hq, nq, d = q.shape
+    group = hq // k.shape[1]
+    sc = _scale(d, scale)
+    out = np.empty((b_, hq, nq), dtype=np.float64)
+    for b in range(b_):
+        for h in range(hq):
+            kf = k[b, h // group].astype(np.float64)
+            for r0 in range(0, nq, chunk_rows):
+                qf = q[b, h, r0:r0 + chunk_rows].astype(np.float64)
+                out[b, h, r0:r0 + chunk_rows] = _lse_rows((qf @ kf.T) * sc)
+    return out
+
+
+def lse_rows_f64(q, k, rows, scale=None):
+    """float64 log-sum-exp for ``rows = [(b, h, i), ...]`` (rows are independent)."""
+    q, k = _np(q), _np(k)
+    hq, d = q.shape[1], q.shape[3]
+    group = hq // k.shape[1]
+    sc = _scale(d, scale)
+    out = np.empty(len(rows), dtype=np.float64)
+    for n, (b, h, i) in enumerate(rows):
+        s = (k[b, h // group].astype(np.float64) @ q[b, h, i].astype(np.float64)) * sc
+        out[n] = _lse_rows(s)
     return out
 
 

@@ -26,6 +26,9 @@ pytestmark = pytest.mark.gpu
 
 ATOL = {"fp32": 2e-3, "fp16": 1e-2}
 RTOL = {"fp32": 2.0 ** -10, "fp16": 1e-2}
+# Log-sum-exp (both variants keep l in FP32): l sums the FP16-rounded
+# probabilities, each within 2^-11 relative, so ln l is within ~4.9e-4.
+LSE_ATOL, LSE_RTOL = 1e-3, 1e-6
 
 
 def say(msg):
@@ -56,6 +59,15 @@ def check(out, exact, acc, what):
     within = bool(np.all(err <= bound))
     assert within, f"{what}: max abs error {worst:.3e} exceeds the bound by {excess:.3e}"
     return worst
+
+
+def check_lse(lse, exact, what):
+    err = np.abs(lse.astype(np.float64) - exact)
+    worst = float(err.max())
+    say(f"  {what} lse max_abs={worst:.3e}")
+    assert bool(np.all(np.isfinite(lse))), f"{what}: non-finite lse"
+    within = bool(np.all(err <= LSE_ATOL + LSE_RTOL * np.abs(exact)))
+    assert within, f"{what}: lse error {worst:.3e}"
 
 
 def inputs(case, seed=0):
@@ -144,6 +156,60 @@ def test_deterministic_and_permutation_invariant(ops):
     assert float((a.float() - c.float()).abs().max()) <= 1e-3
 
 
+RAGGED = [(1, 2, 1, 1, 1), (1, 2, 1, 300, 1000), (2, 4, 2, 257, 129), (1, 12, 1, 1000, 4095),
+          (1, 3, 1, 100, 200), (1, 2, 2, 511, 64), (1, 4, 1, 64, 130)]
+
+
+@pytest.mark.parametrize("acc", ["fp32", "fp16"])
+@pytest.mark.parametrize("b,hq,hkv,nq,nk", RAGGED)
+def test_ragged_tails_and_lse(ops, b, hq, hkv, nq, nk, acc):
+    say(f"case ragged B{b} Hq{hq} Hkv{hkv} nq={nq} nk={nk} acc={acc}")
+    g = torch.Generator().manual_seed(nq * 7 + nk)
+    q = torch.randn(b, hq, nq, 128, generator=g, dtype=torch.float16)
+    k = torch.randn(b, hkv, nk, 128, generator=g, dtype=torch.float16)
+    v = torch.randn(b, hkv, nk, 128, generator=g, dtype=torch.float16)
+    out, lse = ops[acc](q.cuda(), k.cuda(), v.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    check(out.float().cpu().numpy(), orc.attention_f64(q, k, v), acc, "ragged")
+    check_lse(lse.cpu().numpy(), orc.lse_f64(q, k), "ragged")
+
+
+def test_ragged_stress_and_repeat(ops):
+    say("case ragged stress nq=777 nk=1537")
+    g = torch.Generator().manual_seed(77)
+    q = (torch.randn(1, 6, 777, 128, generator=g) * 3).half()
+    k = (torch.randn(1, 2, 1537, 128, generator=g) * 3).half()
+    v = torch.randn(1, 2, 1537, 128, generator=g).half()
+    v[:, :, ::19] *= 8
+    exact = orc.attention_f64(q, k, v)
+    dev = [t.cuda() for t in (q, k, v)]
+    for acc, op in ops.items():
+        first = op(*dev).clone()
+        again = op(*dev).clone()          # the padded workspace is rebuilt each call
+        torch.cuda.synchronize()
+        assert bool(torch.equal(first, again)), acc
+        check(first.float().cpu().numpy(), exact, acc, "ragged stress")
+
+
+def test_lse_every_tile_and_plain_fa_fwd_unchanged(library_path):
+    say("case lse per tile nq=512 nk=1024")
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, 4, 512, 128, generator=g, dtype=torch.float16)
+    k = torch.randn(1, 1, 1024, 128, generator=g, dtype=torch.float16)
+    v = torch.randn(1, 1, 1024, 128, generator=g, dtype=torch.float16)
+    exact_lse = orc.lse_f64(q, k)
+    dev = [t.cuda() for t in (q, k, v)]
+    for kernel in kernel_ids():
+        for acc in ("fp32", "fp16"):
+            op = Operator(library_path, AttentionConfig(acc=acc, kernel=kernel))
+            out, lse = op(*dev, return_lse=True)
+            out = out.clone()
+            plain = op(*dev)              # fa_fwd: same O without the lse output
+            torch.cuda.synchronize()
+            assert bool(torch.equal(out, plain)), (kernel, acc)
+            check_lse(lse.cpu().numpy(), exact_lse, f"tile{kernel} {acc}")
+
+
 def kernel_ids():
     """Every tile configuration the built library offers (collection-time query)."""
     from fa_amd import binding, build
@@ -155,18 +221,26 @@ def kernel_ids():
 
 
 def tile_of(kernel):
+    """(query rows, keys) of one workgroup block of tile configuration ``kernel``,
+    from its name: w{waves}_r{rows per wave}_n{keys} or pp_n{keys}_r{ring} (256 rows)."""
     from fa_amd import binding, build
 
-    op = binding.Operator(build.LIBRARY, binding.AttentionConfig(kernel=kernel))
-    return op.tile((1, 12, 1 << 20, 128), (1, 1, 1 << 20, 128))
+    name = binding.load_library(build.LIBRARY).fa_kernel_name(kernel).decode()
+    parts = dict((p[0], int(p[1:])) for p in name.split("_")[1:])
+    if name.startswith("pp_"):
+        return 256, parts["n"]
+    return int(name.split("_")[0][1:]) * parts["r"], parts["n"]
 
 
-@pytest.mark.parametrize("shape", ["long", "one_block", "stress"])
+@pytest.mark.parametrize("shape", ["long", "one_block", "stress", "ragged"])
 @pytest.mark.parametrize("kernel", kernel_ids())
 def test_every_tile_config(library_path, kernel, shape):
     rows, keys = tile_of(kernel)
+    if shape == "ragged" and not kernel_name(kernel).startswith("pp_"):
+        pytest.skip("plain tiles need whole query and key blocks")
     nq, nk, stress = {"long": (2048, 2048, False), "one_block": (2 * rows, keys, False),
-                      "stress": (rows, 3 * keys, True)}[shape]
+                      "stress": (rows, 3 * keys, True),
+                      "ragged": (rows + 37, 2 * keys + 5, True)}[shape]
     say(f"case tile config {kernel} ({rows}x{keys}) nq={nq} nk={nk} stress={stress}")
     g = torch.Generator().manual_seed(kernel * 7 + nk)
     sig = 3.0 if stress else 1.0
@@ -180,6 +254,12 @@ def test_every_tile_config(library_path, kernel, shape):
         check(run(op, dev), exact, acc, f"tile{kernel}")
 
 
+def kernel_name(kernel):
+    from fa_amd import binding, build
+
+    return binding.load_library(build.LIBRARY).fa_kernel_name(kernel).decode()
+
+
 FULL = [(i, acc) for i in (1, 2, 3, 4) for acc in VARIANTS[i]]
 
 
@@ -189,7 +269,7 @@ def test_full_size_sampled_rows(ops, idx, acc):
     say(f"case c{idx} {case.name} acc={acc}: generating inputs")
     cpu, dev = inputs(case)
     say(f"case c{idx} {case.name} acc={acc}: launching")
-    out = ops[acc](dev["q"], dev["k"], dev["v"])
+    out, lse = ops[acc](dev["q"], dev["k"], dev["v"], return_lse=True)
     torch.cuda.synchronize()
     rows = orc.sample_rows(cpu["q"].shape, 96, seed=idx)
     idx_t = torch.tensor(rows)
@@ -197,6 +277,8 @@ def test_full_size_sampled_rows(ops, idx, acc):
     assert bool(np.all(np.isfinite(out.float().abs().amax(dim=(2, 3)).cpu().numpy())))
     exact = orc.attention_rows_f64(cpu["q"], cpu["k"], cpu["v"], rows)
     check(got, exact, acc, f"c{idx} sampled rows")
+    got_lse = lse[idx_t[:, 0], idx_t[:, 1], idx_t[:, 2]].cpu().numpy()
+    check_lse(got_lse, orc.lse_rows_f64(cpu["q"], cpu["k"], rows), f"c{idx} sampled rows")
     del dev, out
     torch.cuda.empty_cache()
 

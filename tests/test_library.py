@@ -58,7 +58,7 @@ def test_workspace_size(lib):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(batch=0), 2), (dict(heads_q=12, heads_kv=5), 2), (dict(seq_k=-64), 2),
-    (dict(dim=64), 3), (dict(seq_q=4000), 4), (dict(seq_k=4100), 4),
+    (dict(dim=64), 3), (dict(seq_q=4000, kernel=1), 4), (dict(seq_k=4100, kernel=2), 4),
     (dict(acc=2), 7), (dict(scale=0.0), 8), (dict(scale=float("inf")), 8),
     (dict(kernel=99), 9), (dict(reserved=1), 9), (dict(seq_q=1 << 30), 2),
 ])
@@ -66,6 +66,27 @@ def test_geometry_errors(lib, kw, code):
     rc, _ = ws_bytes(lib, problem(**kw))
     assert rc == code
     assert lib.fa_strerror(rc)
+
+
+def test_ragged_tails_and_workspace(lib):
+    # The automatic choice masks ragged tails, so any Nq, Nk >= 1 is valid;
+    # a ragged key tail adds zero-padded copies of K and V^T (whole blocks of
+    # the FP32 default tile: 128 keys).
+    for nq, nk in ((1, 1), (300, 1000), (4097, 4095), (256, 129)):
+        rc, size = ws_bytes(lib, problem(seq_q=nq, seq_k=nk))
+        assert rc == 0, (nq, nk)
+        pad = -(-nk // 128) * 128
+        assert size == 2 * pad * 128 * 2, (nq, nk, size)
+    rc, size = ws_bytes(lib, problem(seq_q=300, seq_k=4096))
+    assert rc == 0 and size == 4096 * 128 * 2          # no key tail: V^T only
+    for kernel in (1, 2):                              # plain tiles keep exact tiling
+        assert ws_bytes(lib, problem(seq_q=300, kernel=kernel))[0] == 4
+        rows, keys = C.c_int32(), C.c_int32()
+        assert lib.fa_fwd_tile(C.byref(problem(kernel=kernel)), C.byref(rows), C.byref(keys)) == 0
+        assert rows.value >= 64 and keys.value == 64
+    rows, keys = C.c_int32(), C.c_int32()
+    assert lib.fa_fwd_tile(C.byref(problem()), C.byref(rows), C.byref(keys)) == 0
+    assert (rows.value, keys.value) == (1, 1)
 
 
 def test_fwd_rejects_before_launch(lib):
@@ -79,6 +100,9 @@ def test_fwd_rejects_before_launch(lib):
     odd = C.c_void_p(4096 + 8)
     assert lib.fa_fwd(C.byref(prob), p, odd, p, p, p, size, None) == 5
     assert lib.fa_fwd(None, p, p, p, p, p, size, None) == 1
+    # fa_fwd_lse: same checks, plus the lse pointer's alignment (NULL is allowed).
+    assert lib.fa_fwd_lse(C.byref(prob), p, p, p, p, odd, p, size, None) == 5
+    assert lib.fa_fwd_lse(C.byref(prob), None, p, p, p, None, p, size, None) == 1
 
 
 def test_kernel_table(lib):
@@ -90,7 +114,7 @@ def test_kernel_table(lib):
     for i in range(0, n + 1):
         rows, keys = C.c_int32(), C.c_int32()
         assert lib.fa_fwd_tile(C.byref(problem(kernel=i)), C.byref(rows), C.byref(keys)) == 0
-        assert rows.value % 32 == 0 and keys.value % 32 == 0
+        assert (rows.value, keys.value) == (1, 1) or (rows.value % 32 == 0 and keys.value % 32 == 0)
         sel = C.c_int32()
         assert lib.fa_fwd_select(C.byref(problem(kernel=i)), C.byref(sel)) == 0
         assert (sel.value == i) if i else (1 <= sel.value <= n)
@@ -126,7 +150,8 @@ def test_operator_validation_without_gpu(library_path):
            torch.zeros(1, 5, 256, 128, dtype=torch.float16))
     with pytest.raises(ValueError, match=r"\[B,H,N,128\]"):
         op(q[0], k, k)
+    plain = binding.Operator(library_path, binding.AttentionConfig(kernel=1))
     with pytest.raises(ValueError, match="tail"):
-        op(q[:, :, :200], k, k)
+        plain(q[:, :, :200], k, k)
     with pytest.raises(ValueError):
         binding.AttentionConfig(acc="bf16")

@@ -168,3 +168,66 @@ def test_checks_catch_planted_mistakes():
         got = bad(q, k, v)
         assert not (np.allclose(got, truth, rtol=1e-9, atol=1e-12)
                     and np.allclose(got, sd, rtol=1e-9, atol=1e-12)), bad.__name__
+
+
+# --------------------------------------------------------------------------- #
+# log-sum-exp
+# --------------------------------------------------------------------------- #
+def lse_checks(lse_fn, q, k, v):
+    """The pinning checks of the LSE oracle; True when every check passes."""
+    import torch
+
+    d = q.shape[3]
+    sc = d ** -0.5
+    group = q.shape[1] // k.shape[1]
+    got = lse_fn(q, k)
+    # torch.logsumexp in float64, the library routine.
+    qt = torch.from_numpy(q.astype(np.float64))
+    kt = torch.from_numpy(np.repeat(k, group, axis=1).astype(np.float64))
+    ref = torch.logsumexp(qt @ kt.transpose(-1, -2) * sc, dim=-1).numpy()
+    ok = np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+    # Softmax identity: O = sum_j exp(scale s_j - lse) v_j.
+    s = np.einsum("bhid,bhjd->bhij", q.astype(np.float64),
+                  np.repeat(k, group, axis=1).astype(np.float64)) * sc
+    o = np.einsum("bhij,bhjd->bhid", np.exp(s - got[..., None]),
+                  np.repeat(v, group, axis=1).astype(np.float64))
+    ok &= np.allclose(o, orc.attention_f64(q, k, v), rtol=1e-10, atol=1e-12)
+    return bool(ok)
+
+
+def test_lse_closed_forms():
+    q, k, v = rand_qkv(1, 2, 1, 5, 1, 16, seed=31)
+    sc = 16 ** -0.5
+    # One key: lse = scale * q . k.
+    want = np.einsum("bhid,bjd->bhi", q.astype(np.float64), k[:, 0].astype(np.float64)) * sc
+    assert np.allclose(orc.lse_f64(q, k), want, rtol=1e-12, atol=1e-12)
+    # Nk identical keys: lse = ln Nk + scale * q . k.
+    kk = np.repeat(k, 7, axis=2)
+    assert np.allclose(orc.lse_f64(q, kk), want + np.log(7), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 1, 9, 13, 16), (2, 4, 2, 6, 33, 8)])
+def test_lse_against_library_and_identity(shape):
+    q, k, v = rand_qkv(*shape, seed=37)
+    assert lse_checks(orc.lse_f64, q, k, v)
+    rows = [(0, 0, 0), (shape[0] - 1, shape[1] - 1, shape[3] - 1), (0, shape[1] - 1, 2)]
+    full = orc.lse_f64(q, k)
+    got = orc.lse_rows_f64(q, k, rows)
+    assert np.allclose(got, [full[r] for r in rows], rtol=0, atol=1e-12)
+
+
+def test_lse_checks_catch_planted_mistakes():
+    q, k, v = rand_qkv(1, 2, 1, 6, 10, 16, seed=41)
+
+    def log2_base(q, k):                   # log2 instead of ln
+        return orc.lse_f64(q, k) / np.log(2)
+
+    def no_scale(q, k):
+        return orc.lse_f64(q, k, scale=1.0)
+
+    def max_only(q, k):                    # drops the log of the sum
+        s = np.einsum("bhid,bjd->bhij", q.astype(np.float64), k[:, 0].astype(np.float64))
+        return s.max(axis=-1) * 16 ** -0.5
+
+    for bad in (log2_base, no_scale, max_only):
+        assert not lse_checks(bad, q, k, v), bad.__name__

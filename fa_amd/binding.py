@@ -47,6 +47,11 @@ SIGNATURES = {
                          C.c_void_p, C.c_uint64, C.c_void_p]),
     "fa_fwd_lse": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                              C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
+    "fa_fwd_capture_count": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_uint64),
+                                       C.POINTER(C.c_int32)]),
+    "fa_fwd_capture": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p,
+                                 C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p,
+                                 C.c_uint64, C.c_void_p]),
     "fa_fwd_tile": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "fa_fwd_select": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32)]),
     "fa_kernel_count": (C.c_int, []),
@@ -67,15 +72,21 @@ def load_library(path):
 
 @dataclass(frozen=True)
 class AttentionConfig:
-    """Launch configuration: accumulation variant and tile selector (0 = automatic)."""
+    """Launch configuration: accumulation variant, tile selector (0 = automatic)
+    and capture (debug) mode, which records every row's online-softmax
+    statistics per key block (the reference config's ``capture`` flag,
+    ``backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/backend.py:27``)."""
     acc: str = "fp32"
     kernel: int = 0
+    capture: bool = False
 
     def __post_init__(self):
         if self.acc not in FA_ACC:
             raise ValueError(f"unknown accumulation variant {self.acc!r}")
         if not isinstance(self.kernel, int) or self.kernel < 0:
             raise ValueError("kernel selector must be a non-negative int")
+        if not isinstance(self.capture, bool):
+            raise ValueError("capture must be a bool")
 
 
 def make_problem(q_shape, k_shape, scale, config):
@@ -92,6 +103,7 @@ class Operator:
         self.lib = load_library(library) if not isinstance(library, C.CDLL) else library
         self.workspace = None
         self.buffers = {}
+        self.last = None
 
     def message(self, status):
         text = self.lib.fa_strerror(status)
@@ -146,9 +158,34 @@ class Operator:
                 self.buffers[key] = torch.empty(q.shape, dtype=torch.float16, device=q.device)
         return self.buffers[key]
 
+    # Capture buffers are for small debug inputs, as in the reference binding
+    # (binding.py:40-42: at most 64 Mi FP32 values).
+    CAPTURE_LIMIT = 64 * 1024 * 1024
+
+    def stats_for(self, q, k, prob):
+        import torch
+
+        key = (tuple(q.shape), tuple(k.shape), q.device, self.config, "stats")
+        if key not in self.buffers:
+            count, block = C.c_uint64(), C.c_int32()
+            self.check(self.lib.fa_fwd_capture_count(C.byref(prob), C.byref(count),
+                                                     C.byref(block)), "capture")
+            if count.value > self.CAPTURE_LIMIT:
+                raise ValueError("debug capture is restricted to small inputs (at most 256 MiB)")
+            nblk = count.value // (4 * q.shape[0] * q.shape[1] * q.shape[2])
+            stats = torch.empty((4, nblk) + tuple(q.shape[:3]), dtype=torch.float32,
+                                device=q.device)
+            self.buffers[key] = (stats, block.value)
+        return self.buffers[key]
+
     def __call__(self, q, k, v, scale=None, return_lse=False):
         """O (cached tensor), or (O, lse) with ``return_lse``: lse [B, Hq, Nq] FP32
-        natural-log log-sum-exp of the scaled scores of each query row."""
+        natural-log log-sum-exp of the scaled scores of each query row.
+
+        With ``config.capture`` the call also fills ``self.last["stats"]``,
+        FP32 [4, nblk, B, Hq, Nq]: per key block of ``self.last["block_keys"]``
+        keys, each row's running max m (natural-log units), running sum l
+        relative to m, rescale factor alpha and block sum z relative to m."""
         import torch
 
         self.validate(q, k, v)
@@ -159,7 +196,9 @@ class Operator:
         size = C.c_uint64()
         self.check(self.lib.fa_fwd_workspace_bytes(C.byref(prob), C.byref(size)), "prepare")
         out = self.buffers_for(q, k)
-        lse = self.buffers_for(q, k, lse=True) if return_lse else None
+        capture = self.config.capture
+        lse = self.buffers_for(q, k, lse=True) if (return_lse or capture) else None
+        stats, block = self.stats_for(q, k, prob) if capture else (None, 0)
         with torch.cuda.device(q.device):
             need = max(size.value, 16)
             if self.workspace is None or self.workspace.device != q.device \
@@ -169,11 +208,16 @@ class Operator:
             common = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
             tail = (self.workspace.data_ptr(), self.workspace.numel(),
                     C.c_void_p(stream.cuda_stream))
-            if return_lse:
+            if capture:
+                status = self.lib.fa_fwd_capture(C.byref(prob), *common, lse.data_ptr(),
+                                                 stats.data_ptr(), stats.numel(), *tail)
+            elif return_lse:
                 status = self.lib.fa_fwd_lse(C.byref(prob), *common, lse.data_ptr(), *tail)
             else:
                 status = self.lib.fa_fwd(C.byref(prob), *common, *tail)
             self.check(status, "launch")
-            for t in (q, k, v, out, self.workspace) + ((lse,) if return_lse else ()):
+            extra = tuple(t for t in (lse, stats) if t is not None)
+            for t in (q, k, v, out, self.workspace) + extra:
                 t.record_stream(stream)
+        self.last = {"output": out, "lse": lse, "stats": stats, "block_keys": block}
         return (out, lse) if return_lse else out

@@ -58,14 +58,20 @@ constexpr float LN2 = 0.6931471805599453f;
 // Kernel arguments. seq_k is the key length of the K and V^T buffers the
 // kernel reads (a multiple of its key block); keys at or past nk_valid are
 // zero padding and masked out of the softmax. lse (FP32 [B, Hq, Nq],
-// natural-log log-sum-exp of the scaled scores) may be null. c is the softmax
-// scale times log2(e).
+// natural-log log-sum-exp of the scaled scores) may be null. stats, when not
+// null, receives the online-softmax statistics of every row after every key
+// block (capture mode, ping-pong tiles): FP32 [4][seq_k / BN][B * Hq * Nq]
+// holding the running max m (natural-log units, scale * score), the running
+// sum l relative to m, the rescale factor alpha applied at that block, and
+// the block's own row sum z relative to m. c is the softmax scale times
+// log2(e).
 struct FaArgs {
   const _Float16* q;
   const _Float16* k;
   const _Float16* vt;
   _Float16* o;
   float* lse;
+  float* stats;
   int heads_q, group, seq_q, seq_k, nk_valid;
   float c;
 };
@@ -419,7 +425,7 @@ __device__ __forceinline__ void lds_barrier() {
 // until a block exceeds it by more than TAU, so P <= 2^TAU and the O/l
 // rescale runs only on the rare blocks where some row of the wave needs it.
 // With TAU = 0 the max tracks every increase (FP16 O must not grow).
-template <bool ACC16, int BN, int NS, bool SPLIT_HI>
+template <bool ACC16, int BN, int NS, bool SPLIT_HI, bool CAPTURE>
 __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   const _Float16* __restrict__ q = args.q;
   const _Float16* __restrict__ k = args.k;
@@ -710,7 +716,20 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
         p[2 * t + g2] = frag;
       }
     }
-    lsum += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    const float zsum = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    lsum += zsum;
+    if constexpr (CAPTURE) {         // capture mode: this block's row statistics
+      const float z = half_sum(zsum), lrow = half_sum(lsum);
+      if (hf == 0 && row_ok) {
+        const size_t rows = (size_t)gridDim.x / tiles_q * seq_q;   // B * Hq * Nq
+        const size_t nb = seq_k / BN, j = key0 / BN;
+        float* st = args.stats + grow;
+        st[(0 * nb + j) * rows] = m * c * LN2;
+        st[(1 * nb + j) * rows] = lrow;
+        st[(2 * nb + j) * rows] = alpha;
+        st[(3 * nb + j) * rows] = z;
+      }
+    }
   };
   auto next = [](int sl) { return sl == NS - 1 ? 0 : sl + 1; };
   auto prev = [](int sl) { return sl == 0 ? NS - 1 : sl - 1; };
@@ -799,25 +818,27 @@ constexpr int pp_lds_bytes(int bn, int ns) { return ns * (bn * (HD * 2 + 16) + H
 template <int KIND, int P1>
 constexpr int kThreads = KIND ? 512 : P1 * 64;
 
-template <bool ACC16, int KIND, int P1, int P2, int BN>
+template <bool ACC16, int KIND, int P1, int P2, int BN, bool CAP>
 __device__ __forceinline__ void fa_dispatch(const FaArgs& args) {
   if constexpr (KIND == 0) fa_fwd_body<ACC16, P1, P2, BN>(args);
-  else fa_pp_body<ACC16, BN, P1, P2 == 1>(args);
+  else fa_pp_body<ACC16, BN, P1, P2 == 1, CAP>(args);
 }
 
 // Device entry points, one per accumulation variant. Their names contain the
 // registry names of the backends that launch them, which is how the profiler
 // attributes kernel time (WPE = waves per SIMD the register budget targets).
-template <int KIND, int P1, int P2, int BN, int WPE>
+// CAP builds the capture-mode variant, a separate kernel so the production
+// kernels carry none of its code.
+template <int KIND, int P1, int P2, int BN, int WPE, bool CAP>
 __global__ void __launch_bounds__((kThreads<KIND, P1>)) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 hip_fa_fp32acc_kernel(FaArgs args) {
-  fa_dispatch<false, KIND, P1, P2, BN>(args);
+  fa_dispatch<false, KIND, P1, P2, BN, CAP>(args);
 }
 
-template <int KIND, int P1, int P2, int BN, int WPE>
+template <int KIND, int P1, int P2, int BN, int WPE, bool CAP>
 __global__ void __launch_bounds__((kThreads<KIND, P1>)) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 hip_fa_fp16acc_kernel(FaArgs args) {
-  fa_dispatch<true, KIND, P1, P2, BN>(args);
+  fa_dispatch<true, KIND, P1, P2, BN, CAP>(args);
 }
 
 // ----------------------------------------------------------------------------
@@ -831,17 +852,21 @@ struct TileConfig {
   int rows;        // BM
   int keys;        // BN
   int lds;         // dynamic LDS bytes per workgroup
-  bool tails;      // masks ragged query and key tails (any Nq, Nk)
+  bool tails;      // masks ragged query and key tails (any Nq, Nk); has capture mode
   attn_fn fp32;
   attn_fn fp16;
+  attn_fn fp32_capture;   // null when the tile has no capture mode
+  attn_fn fp16_capture;
 };
 
 #define FA_TILE(NAME, KIND, P1, P2, BN, WPE)                                                 \
   TileConfig {                                                                             \
     NAME, kThreads<KIND, P1>, (KIND ? 8 : P1 * P2) * 32, BN,                               \
         (KIND ? pp_lds_bytes(BN, P1) : 0), KIND == 1,                                      \
-        &hip_fa_fp32acc_kernel<KIND, P1, P2, BN, WPE>,                                     \
-        &hip_fa_fp16acc_kernel<KIND, P1, P2, BN, WPE>                                      \
+        &hip_fa_fp32acc_kernel<KIND, P1, P2, BN, WPE, false>,                              \
+        &hip_fa_fp16acc_kernel<KIND, P1, P2, BN, WPE, false>,                              \
+        KIND == 1 ? &hip_fa_fp32acc_kernel<KIND, P1, P2, BN, WPE, true> : nullptr,         \
+        KIND == 1 ? &hip_fa_fp16acc_kernel<KIND, P1, P2, BN, WPE, true> : nullptr          \
   }
 
 const TileConfig kTiles[] = {
@@ -928,16 +953,25 @@ int validate(const fa_problem* p, const TileConfig** tile) {
   return FA_OK;
 }
 
+// FP32 values capture mode writes: 4 statistics x key blocks x B * Hq * Nq rows.
+uint64_t capture_count(const fa_problem* p, const TileConfig* tile, const KeyLayout& lay) {
+  return 4ull * (uint64_t)(lay.nk_pad / tile->keys) * (uint64_t)(p->batch * p->heads_q * p->seq_q);
+}
+
 int launch(const fa_problem* p, const void* q, const void* k, const void* v, void* o, float* lse,
-           void* workspace, uint64_t workspace_bytes, void* stream) {
+           float* stats, uint64_t stats_count, void* workspace, uint64_t workspace_bytes,
+           void* stream) {
   const TileConfig* tile = nullptr;
   int rc = validate(p, &tile);
   if (rc) return rc;
   if (!q || !k || !v || !o) return FA_ERR_NULL;
   const KeyLayout lay = key_layout(p, tile);
   if (!workspace || workspace_bytes < lay.vt_bytes + lay.k_bytes) return FA_ERR_WORKSPACE;
-  for (const void* ptr : {q, k, v, (const void*)o, (const void*)workspace, (const void*)lse})
+  for (const void* ptr : {q, k, v, (const void*)o, (const void*)workspace, (const void*)lse,
+                          (const void*)stats})
     if (reinterpret_cast<uintptr_t>(ptr) & 15) return FA_ERR_ALIGN;
+  if (stats && (!tile->fp32_capture || stats_count < capture_count(p, tile, lay)))
+    return FA_ERR_CAPTURE;
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   _Float16* vt = static_cast<_Float16*>(workspace);
@@ -955,6 +989,7 @@ int launch(const fa_problem* p, const void* q, const void* k, const void* v, voi
   args.vt = vt;
   args.o = static_cast<_Float16*>(o);
   args.lse = lse;
+  args.stats = stats;
   args.heads_q = (int)p->heads_q;
   args.group = (int)(p->heads_q / p->heads_kv);
   args.seq_q = (int)p->seq_q;
@@ -963,7 +998,8 @@ int launch(const fa_problem* p, const void* q, const void* k, const void* v, voi
   args.c = (float)((double)p->scale * LOG2E);
   const int64_t tiles_q = (p->seq_q + tile->rows - 1) / tile->rows;
   const unsigned grid = (unsigned)(p->batch * p->heads_q * tiles_q);
-  attn_fn fn = p->acc == FA_ACC_FP16 ? tile->fp16 : tile->fp32;
+  attn_fn fn = stats ? (p->acc == FA_ACC_FP16 ? tile->fp16_capture : tile->fp32_capture)
+                     : (p->acc == FA_ACC_FP16 ? tile->fp16 : tile->fp32);
   if (tile->lds > 65536 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                           hipFuncAttributeMaxDynamicSharedMemorySize, tile->lds) != hipSuccess)
@@ -1008,12 +1044,30 @@ int fa_fwd_select(const fa_problem* p, int32_t* kernel) {
 
 int fa_fwd(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
            void* workspace, uint64_t workspace_bytes, void* stream) {
-  return launch(p, q, k, v, o, nullptr, workspace, workspace_bytes, stream);
+  return launch(p, q, k, v, o, nullptr, nullptr, 0, workspace, workspace_bytes, stream);
 }
 
 int fa_fwd_lse(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
                float* lse, void* workspace, uint64_t workspace_bytes, void* stream) {
-  return launch(p, q, k, v, o, lse, workspace, workspace_bytes, stream);
+  return launch(p, q, k, v, o, lse, nullptr, 0, workspace, workspace_bytes, stream);
+}
+
+int fa_fwd_capture_count(const fa_problem* p, uint64_t* count, int32_t* block_keys) {
+  if (!count || !block_keys) return FA_ERR_NULL;
+  const TileConfig* tile = nullptr;
+  int rc = validate(p, &tile);
+  if (rc) return rc;
+  if (!tile->fp32_capture) return FA_ERR_CAPTURE;
+  *count = capture_count(p, tile, key_layout(p, tile));
+  *block_keys = tile->keys;
+  return FA_OK;
+}
+
+int fa_fwd_capture(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
+                   float* lse, float* stats, uint64_t stats_count, void* workspace,
+                   uint64_t workspace_bytes, void* stream) {
+  if (!stats) return FA_ERR_NULL;
+  return launch(p, q, k, v, o, lse, stats, stats_count, workspace, workspace_bytes, stream);
 }
 
 int fa_kernel_count(void) { return kNumTiles; }
@@ -1036,6 +1090,7 @@ const char* fa_strerror(int status) {
     case FA_ERR_SCALE: return "scale must be finite and positive";
     case FA_ERR_KERNEL: return "unknown kernel selector";
     case FA_ERR_LAUNCH: return "HIP kernel launch failed";
+    case FA_ERR_CAPTURE: return "capture needs a ping-pong tile and a stats buffer of fa_fwd_capture_count() floats";
     default: return "unknown status";
   }
 }

@@ -41,7 +41,8 @@ enum fa_status {
   FA_ERR_ACC = 7,           /* unknown accumulation variant */
   FA_ERR_SCALE = 8,         /* scale not finite and positive */
   FA_ERR_KERNEL = 9,        /* unknown kernel selector */
-  FA_ERR_LAUNCH = 10        /* the HIP runtime rejected a launch */
+  FA_ERR_LAUNCH = 10,       /* the HIP runtime rejected a launch */
+  FA_ERR_CAPTURE = 11       /* capture asked of a tile without it, or stats buffer too small */
 };
 
 enum fa_acc {
@@ -94,6 +95,27 @@ int fa_fwd(const fa_problem* p, const void* q, const void* k, const void* v, voi
  */
 int fa_fwd_lse(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
                float* lse, void* workspace, uint64_t workspace_bytes, void* stream);
+
+/*
+ * Capture (debug) mode: fa_fwd_lse() that also records the online-softmax
+ * statistics of every query row after every key block of the selected tile,
+ * the counterpart of the reference's capture flag, which dumps the running
+ * max, running sum, rescale factor and block row sum per packet into its
+ * stats buffer (binding.py:40-44, K32/vector_output.h:29-36). Layout: FP32
+ * stats[4][nblk][B * Hq * Nq] (row index (b * Hq + h) * Nq + i), in order
+ *   m      running max after the block, natural-log units (scale * score);
+ *   l      running sum after the block, relative to m;
+ *   alpha  factor the previous sum and O were rescaled by at the block;
+ *   z      the block's own sum of (FP16-rounded) probabilities, relative to m;
+ * so m + ln l is the log-sum-exp of every key so far and m + ln z that of
+ * the block. fa_fwd_capture_count() gives the float count and the block size
+ * (key blocks nblk = ceil(Nk / block_keys)). Ping-pong tiles only (the
+ * automatic choice); meant for small debug inputs.
+ */
+int fa_fwd_capture_count(const fa_problem* p, uint64_t* count, int32_t* block_keys);
+int fa_fwd_capture(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
+                   float* lse, float* stats, uint64_t stats_count, void* workspace,
+                   uint64_t workspace_bytes, void* stream);
 
 /*
  * Query-row and key granularity the kernel fa_fwd() would use for *p needs:

@@ -40,6 +40,14 @@ Functions and what pins each (tests/test_oracle.py):
                        closed forms (one key, identical keys), torch.logsumexp
                        in float64, and the identity attention_f64 ==
                        sum_j exp(scale s_j - lse) v_j.
+  block_stats_f64      exact per-key-block statistics the capture mode's
+                       online softmax must reproduce: log-sum-exp and max of
+                       the scaled scores over each block and over every key
+                       up to the block's end (the quantities behind the
+                       reference's per-packet m, l, alpha and row-sum dumps,
+                       K32/vector_output.h:22-38); pinned by the last prefix
+                       equalling lse_f64, each block equalling lse_f64 of its
+                       key slice, and the logaddexp recursion of the prefixes.
 Every check above plants a mistake in the oracle (dropped scale, swapped GQA
 map, transposed operand) and confirms at least one check fails
 (tests/test_oracle.py::test_checks_catch_planted_mistakes).
@@ -179,6 +187,35 @@ def lse_rows_f64(q, k, rows, scale=None):
     for n, (b, h, i) in enumerate(rows):
         s = (k[b, h // group].astype(np.float64) @ q[b, h, i].astype(np.float64)) * sc
         out[n] = _lse_rows(s)
+    return out
+
+
+def block_stats_f64(q, k, block, scale=None):
+    """Exact statistics per key block of ``block`` keys (the last may be ragged).
+
+    Returns float64 arrays of shape [nblk, B, Hq, Nq]:
+      lse_prefix  ln sum exp(scale s_j) over keys j < min((n+1) * block, Nk)
+      lse_block   ln sum exp(scale s_j) over block n's keys
+      max_prefix  max scale * s_j over the prefix
+      max_block   max scale * s_j over block n
+    """
+    q, k = _np(q), _np(k)
+    b_, hq, nq, d = q.shape
+    nk = k.shape[2]
+    group = hq // k.shape[1]
+    sc = _scale(d, scale)
+    nblk = -(-nk // block)
+    out = {n: np.empty((nblk, b_, hq, nq)) for n in ("lse_prefix", "lse_block", "max_prefix", "max_block")}
+    for b in range(b_):
+        for h in range(hq):
+            s = (q[b, h].astype(np.float64) @ k[b, h // group].astype(np.float64).T) * sc
+            for n in range(nblk):
+                blk = s[:, n * block:(n + 1) * block]
+                pre = s[:, :(n + 1) * block]
+                out["lse_block"][n, b, h] = _lse_rows(blk)
+                out["lse_prefix"][n, b, h] = _lse_rows(pre)
+                out["max_block"][n, b, h] = blk.max(axis=-1)
+                out["max_prefix"][n, b, h] = pre.max(axis=-1)
     return out
 
 

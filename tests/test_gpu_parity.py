@@ -210,6 +210,50 @@ def test_lse_every_tile_and_plain_fa_fwd_unchanged(library_path):
             check_lse(lse.cpu().numpy(), exact_lse, f"tile{kernel} {acc}")
 
 
+CAPTURE = [(1, 4, 1, 96, 1000), (2, 2, 2, 257, 129), (1, 3, 1, 64, 64), (1, 2, 1, 300, 2048)]
+
+
+@pytest.mark.parametrize("acc", ["fp32", "fp16"])
+@pytest.mark.parametrize("b,hq,hkv,nq,nk", CAPTURE)
+def test_capture_statistics(library_path, b, hq, hkv, nq, nk, acc):
+    """Capture-mode per-block m, l, alpha, z against the exact block statistics."""
+    say(f"case capture B{b} Hq{hq} Hkv{hkv} nq={nq} nk={nk} acc={acc}")
+    g = torch.Generator().manual_seed(nq + 3 * nk)
+    sig = 2.0 if nq == 300 else 1.0                # wider logits: several max updates
+    q = (torch.randn(b, hq, nq, 128, generator=g) * sig).half()
+    k = (torch.randn(b, hkv, nk, 128, generator=g) * sig).half()
+    v = torch.randn(b, hkv, nk, 128, generator=g).half()
+    op = Operator(library_path, AttentionConfig(acc=acc, capture=True))
+    out, lse = op(q.cuda(), k.cuda(), v.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    m, l, alpha, z = (t.double().cpu().numpy() for t in op.last["stats"])
+    ex = orc.block_stats_f64(q, k, op.last["block_keys"])
+    assert m.shape == ex["lse_prefix"].shape
+    check(out.float().cpu().numpy(), orc.attention_f64(q, k, v), acc, "capture O")
+    # m + ln l is the log-sum-exp of every key so far; the last one is lse.
+    assert bool(np.all(np.abs(m + np.log(l) - ex["lse_prefix"]) <= LSE_ATOL))
+    assert bool(np.all(np.abs(lse.cpu().numpy() - (m[-1] + np.log(l[-1]))) <= 1e-5))
+    # z is the block's own mass relative to m, exp(lse_block - m), summed over
+    # FP16-rounded probabilities: each within 2^-11 relative when normal and
+    # within 2^-25 absolute in the subnormal range, so per block
+    # |z - exact| <= 1e-3 * exact + block_keys * 2^-24.
+    zx = np.exp(ex["lse_block"] - m)
+    zbound = LSE_ATOL * zx + op.last["block_keys"] * 2.0 ** -24
+    assert bool(np.all(np.abs(z - zx) <= zbound)), float(np.abs(z - zx).max())
+    # Recurrences: alpha = exp(m_prev - m), l = alpha * l_prev + z.
+    assert bool(np.allclose(alpha[1:], np.exp(m[:-1] - m[1:]), rtol=1e-5, atol=1e-30))
+    assert bool(np.allclose(l[1:], alpha[1:] * l[:-1] + z[1:], rtol=1e-5, atol=0))
+    # The running max never falls; FP16 O tracks the exact prefix max, FP32 O
+    # raises it lazily (at most 8 log2 units, i.e. P <= 2^8, below the max).
+    assert bool(np.all(np.diff(m, axis=0) >= 0))
+    tol = 1e-4 * np.abs(ex["max_prefix"]) + 1e-4
+    assert bool(np.all(m <= ex["max_prefix"] + tol))
+    lag = 0.0 if acc == "fp16" else 8 * np.log(2)
+    assert bool(np.all(ex["max_prefix"] - m <= lag + tol))
+    say(f"  capture acc={acc} blocks={m.shape[0]} max|m+ln l-lse|="
+        f"{float(np.abs(m + np.log(l) - ex['lse_prefix']).max()):.2e}")
+
+
 def kernel_ids():
     """Every tile configuration the built library offers (collection-time query)."""
     from fa_amd import binding, build

@@ -89,6 +89,28 @@ def test_ragged_tails_and_workspace(lib):
     assert (rows.value, keys.value) == (1, 1)
 
 
+def test_capture_count_and_rejections(lib):
+    prob = problem(seq_q=300, seq_k=1000)            # FP32 default tile: 128-key blocks
+    count, block = C.c_uint64(), C.c_int32()
+    assert lib.fa_fwd_capture_count(C.byref(prob), C.byref(count), C.byref(block)) == 0
+    assert block.value == 128 and count.value == 4 * 8 * 12 * 300
+    prob16 = problem(seq_q=300, seq_k=1000, acc=1)   # FP16 default tile: 64-key blocks
+    assert lib.fa_fwd_capture_count(C.byref(prob16), C.byref(count), C.byref(block)) == 0
+    assert block.value == 64 and count.value == 4 * 16 * 12 * 300
+    plain = problem(kernel=1)                        # plain tiles have no capture mode
+    assert lib.fa_fwd_capture_count(C.byref(plain), C.byref(count), C.byref(block)) == 11
+    assert lib.fa_fwd_capture_count(C.byref(prob), None, C.byref(block)) == 1
+    # Launch-time checks happen on the host, before any GPU work.
+    p = C.c_void_p(4096)
+    _, size = ws_bytes(lib, prob)
+    need = 4 * 8 * 12 * 300
+    assert lib.fa_fwd_capture(C.byref(prob), p, p, p, p, None, None, need, p, size, None) == 1
+    assert lib.fa_fwd_capture(C.byref(prob), p, p, p, p, None, p, need - 1, p, size, None) == 11
+    _, psize = ws_bytes(lib, plain)
+    assert lib.fa_fwd_capture(C.byref(plain), p, p, p, p, None, p, 1 << 40, p, psize, None) == 11
+    assert lib.fa_strerror(11)
+
+
 def test_fwd_rejects_before_launch(lib):
     prob = problem()
     # NULL tensors, missing workspace and misaligned pointers fail on the host.

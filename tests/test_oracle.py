@@ -231,3 +231,43 @@ def test_lse_checks_catch_planted_mistakes():
 
     for bad in (log2_base, no_scale, max_only):
         assert not lse_checks(bad, q, k, v), bad.__name__
+
+
+# --------------------------------------------------------------------------- #
+# per-block statistics (capture mode)
+# --------------------------------------------------------------------------- #
+def block_checks(stats, q, k, block):
+    """True when per-block statistics agree with lse_f64 on key slices."""
+    nk = k.shape[2]
+    ok = np.allclose(stats["lse_prefix"][-1], orc.lse_f64(q, k), rtol=0, atol=1e-10)
+    for n in range(stats["lse_block"].shape[0]):
+        sl = k[:, :, n * block:min((n + 1) * block, nk)]
+        ok &= np.allclose(stats["lse_block"][n], orc.lse_f64(q, sl), rtol=0, atol=1e-10)
+        if n:
+            ok &= np.allclose(stats["lse_prefix"][n],
+                              np.logaddexp(stats["lse_prefix"][n - 1], stats["lse_block"][n]),
+                              rtol=0, atol=1e-10)
+    ok &= np.allclose(stats["max_prefix"], np.maximum.accumulate(stats["max_block"], axis=0))
+    return bool(ok)
+
+
+@pytest.mark.parametrize("nk,block", [(64, 64), (200, 64), (129, 128), (7, 128)])
+def test_block_stats(nk, block):
+    q, k, _ = rand_qkv(1, 4, 2, 5, nk, 16, seed=nk)
+    st = orc.block_stats_f64(q, k, block)
+    assert st["lse_block"].shape == (-(-nk // block), 1, 4, 5)
+    assert block_checks(st, q, k, block)
+
+
+def test_block_stats_catch_planted_mistakes():
+    q, k, _ = rand_qkv(1, 2, 1, 4, 200, 16, seed=5)
+    good = orc.block_stats_f64(q, k, 64)
+
+    shifted = {n: a.copy() for n, a in good.items()}            # blocks start one key late
+    alt = orc.block_stats_f64(q, k[:, :, 1:], 64)
+    shifted["lse_block"][:alt["lse_block"].shape[0]] = alt["lse_block"]
+    no_scale = orc.block_stats_f64(q, k, 64, scale=1.0)
+    swapped = {n: a.copy() for n, a in good.items()}            # prefix and block exchanged
+    swapped["lse_prefix"], swapped["lse_block"] = good["lse_block"], good["lse_prefix"]
+    for bad in (shifted, no_scale, swapped):
+        assert not block_checks(bad, q, k, 64)

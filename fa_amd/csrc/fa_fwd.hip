@@ -3,12 +3,15 @@
 //
 // Work decomposition (reference: task = (batch*head, query block), KV head
 // = head / group, backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/project/
-// op_kernel/panel_kernel.h:264-274): one workgroup owns BM = NW*SUB*32 query
-// rows of one (batch, head); each wave owns SUB subtiles of 32 rows. The
-// workgroup streams the whole key range in blocks of BN keys; each K block
-// and V^T block is staged once in LDS (double-buffered) and read by every
-// wave, and every wave keeps its Q fragments, O accumulators and softmax
-// statistics in registers for the whole key loop.
+// op_kernel/panel_kernel.h:264-274): one workgroup owns BM query rows of one
+// (batch, head) (BM = 256: the ping-pong body's 8 waves x 32 rows, or the
+// plain body's NW waves x SUB subtiles of 32 rows). The workgroup streams the
+// whole key range in blocks of BN keys; each K block and V^T block is staged
+// once in LDS (a ring of slots) and read by every wave, and every wave keeps
+// its Q fragments, O accumulators and softmax statistics in registers for the
+// whole key loop. The ping-pong body also masks ragged query and key tails,
+// writes the per-row log-sum-exp on request, and has a capture variant that
+// records the per-block softmax statistics.
 //
 // Matrix products run transposed so the softmax is lane-local:
 //   S^T = K Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS, B = Q^T
@@ -19,9 +22,9 @@
 //                 for all its O registers, so rescaling by alpha is per lane.
 // The 32x32 output layout gives a lane keys {8g+4h .. 8g+4h+3} (g = 0..3,
 // h = lane/32); the PV step over keys 16s..16s+15 therefore wants, in its k
-// slots 8h..8h+7, keys {16s+4h..+3, 16s+8+4h..+3}. The V transpose kernel
-// writes V^T with exactly that key order inside every 16-key group, so each
-// A fragment is one 16-byte LDS read.
+// slots 8h..8h+7, keys {16s+4h..+3, 16s+8+4h..+3}. The prep kernel writes
+// V^T with exactly that key order inside every 16-key group, so each A
+// fragment is one 16-byte LDS read.
 //
 // Online softmax in base 2 with the scale folded in (c = scale*log2(e)):
 //   m' = max(m, rowmax(S)),  alpha = 2^((m - m') c),  P = 2^(S c - m' c),
@@ -36,8 +39,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
-
-#include <type_traits>
 
 #include "../../include/fa_hip.h"
 

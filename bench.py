@@ -129,7 +129,7 @@ def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(the attention path shards without communication; see DESIGN.md)",
+              "(one GPU only; query tiles would shard across GPUs without communication)",
               file=sys.stderr)
         return 2
 

@@ -51,7 +51,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int HD = 128;               // head dimension
-constexpr int VT_GROUP = 64;          // keys per V-transpose workgroup
+constexpr int VT_GROUP = 64;          // keys per prep-kernel workgroup
 constexpr float NEG_BIG = -1.0e30f;   // finite "minus infinity" for the running max
 constexpr double LOG2E = 1.4426950408889634;
 constexpr float LN2 = 0.6931471805599453f;

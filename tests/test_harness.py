@@ -356,7 +356,7 @@ class ProfileNameTests(unittest.TestCase):
         k16 = k32.replace("fp32acc", "fp16acc")
         self.assertEqual(profiler._match_backend(k32, names, op_types, {}), "hip_fa_fp32acc")
         self.assertEqual(profiler._match_backend(k16, names, op_types, {}), "hip_fa_fp16acc")
-        self.assertIsNone(profiler._match_backend("fa_vt_kernel", names, op_types, {}))
+        self.assertIsNone(profiler._match_backend("fa_prep_kernel", names, op_types, {}))
 
     def test_kernel_trace_averages(self):
         with tempfile.NamedTemporaryFile("w", suffix=".csv", delete=False) as f:

@@ -56,11 +56,11 @@ def test_kernel_stats_from_rocpd_db(tmp_path):
     con = sqlite3.connect(db)
     con.execute("CREATE TABLE kernels (name TEXT, duration INTEGER)")
     con.executemany("INSERT INTO kernels VALUES (?, ?)",
-                    [("hip_fa_fp32acc_kernel", 100), ("hip_fa_fp32acc_kernel", 300), ("fa_vt", 10)])
+                    [("hip_fa_fp32acc_kernel", 100), ("hip_fa_fp32acc_kernel", 300), ("fa_prep", 10)])
     con.commit()
     con.close()
     stats = kernel_stats.collect(str(tmp_path / "out"))
-    assert stats == {"hip_fa_fp32acc_kernel": [100.0, 300.0], "fa_vt": [10.0]}
+    assert stats == {"hip_fa_fp32acc_kernel": [100.0, 300.0], "fa_prep": [10.0]}
     text = kernel_stats.render(stats, flops=2e9, match="hip_fa_fp32acc")
     # 2e9 FLOP / 200 ns average = 1e16 FLOP/s = 10000 TFLOP/s
     assert "10000.0 TFLOP/s" in text

@@ -951,6 +951,8 @@ int validate(const fa_problem* p, const TileConfig** tile) {
   const int64_t tiles_q = (p->seq_q + (*tile)->rows - 1) / (*tile)->rows;
   if (bh >= lim || bh * tiles_q >= lim || p->batch * p->heads_kv >= 65536) return FA_ERR_GEOMETRY;
   if (!tile_fits(**tile, p)) return FA_ERR_TAIL;
+  // The kernels address a V^T row (Nk' keys) with 32-bit byte offsets.
+  if ((int64_t)HD * 2 * key_layout(p, *tile).nk_pad >= ((int64_t)1 << 31)) return FA_ERR_GEOMETRY;
   return FA_OK;
 }
 

@@ -174,6 +174,33 @@ def test_ragged_tails_and_lse(ops, b, hq, hkv, nq, nk, acc):
     check_lse(lse.cpu().numpy(), orc.lse_f64(q, k), "ragged")
 
 
+def _random_shapes(n, seed=2024):
+    import random
+
+    rng = random.Random(seed)
+    out = []
+    for _ in range(n):
+        hkv = rng.choice([1, 2, 4])
+        out.append((rng.choice([1, 2, 3]), hkv * rng.choice([1, 2, 3]), hkv,
+                    rng.randint(1, 1500), rng.randint(1, 2500)))
+    return out
+
+
+@pytest.mark.parametrize("b,hq,hkv,nq,nk", _random_shapes(6))
+def test_random_shapes_both_variants(ops, b, hq, hkv, nq, nk):
+    say(f"case random B{b} Hq{hq} Hkv{hkv} nq={nq} nk={nk}")
+    g = torch.Generator().manual_seed(b * 1000003 + nq * 101 + nk)
+    q = torch.randn(b, hq, nq, 128, generator=g, dtype=torch.float16)
+    k = torch.randn(b, hkv, nk, 128, generator=g, dtype=torch.float16)
+    v = torch.randn(b, hkv, nk, 128, generator=g, dtype=torch.float16)
+    exact = orc.attention_f64(q, k, v)
+    dev = [t.cuda() for t in (q, k, v)]
+    for acc, op in ops.items():
+        out = op(*dev)
+        torch.cuda.synchronize()
+        check(out.float().cpu().numpy(), exact, acc, "random")
+
+
 def test_ragged_stress_and_repeat(ops):
     say("case ragged stress nq=777 nk=1537")
     g = torch.Generator().manual_seed(77)

@@ -89,6 +89,12 @@ def test_ragged_tails_and_workspace(lib):
     assert (rows.value, keys.value) == (1, 1)
 
 
+def test_key_length_limit(lib):
+    # V^T rows are addressed with 32-bit byte offsets: 128 rows x Nk' keys x 2 B < 2^31.
+    assert ws_bytes(lib, problem(seq_q=256, seq_k=8_000_000))[0] == 0
+    assert ws_bytes(lib, problem(seq_q=256, seq_k=9_000_000))[0] == 2
+
+
 def test_capture_count_and_rejections(lib):
     prob = problem(seq_q=300, seq_k=1000)            # FP32 default tile: 128-key blocks
     count, block = C.c_uint64(), C.c_int32()

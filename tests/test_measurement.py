@@ -77,3 +77,16 @@ def test_bench_reads_the_committed_traffic_summary():
     value = bench.traffic_from_profiles(key)
     assert isinstance(value, int) and value > 1_677_721_600   # at least the algorithmic bytes
     assert bench.traffic_from_profiles(key + "x") is None
+
+
+def test_counter_summary(tmp_path):
+    from fa_amd.core import counters
+
+    write_counters(tmp_path / "c", "SQ_BUSY_CYCLES", [(1, "hip_fa_fp32acc_kernel", 5.0),
+                                                      (1, "hip_fa_fp32acc_kernel", 7.0),
+                                                      (2, "hip_fa_fp32acc_kernel", 10.0),
+                                                      (3, "fa_prep_kernel", 1.0)])
+    assert counters.counter_names(str(tmp_path / "c")) == ["SQ_BUSY_CYCLES"]
+    s = counters.summarize(str(tmp_path / "c"), "hip_fa_", ["SQ_BUSY_CYCLES"])
+    val, n, kernel = s["SQ_BUSY_CYCLES"]
+    assert (n, kernel) == (2, "hip_fa_fp32acc_kernel") and val == 11.0   # median of 12, 10

@@ -23,6 +23,11 @@ import math
 from dataclasses import dataclass
 
 FA_ACC = {"fp32": 0, "fp16": 1}
+# Attention masks (enum fa_causal): full attention, the reference's only mode,
+# or a causal mask aligned top-left (key j <= query i, torch's
+# scaled_dot_product_attention(is_causal=True)) or bottom-right
+# (j <= i + Nk - Nq).
+FA_CAUSAL = {"none": 0, "top_left": 1, "bottom_right": 2}
 
 
 class FaProblem(C.Structure):
@@ -36,7 +41,7 @@ class FaProblem(C.Structure):
         ("scale", C.c_float),
         ("acc", C.c_int32),
         ("kernel", C.c_int32),
-        ("reserved", C.c_int32),
+        ("causal", C.c_int32),
     ]
 
 
@@ -72,13 +77,16 @@ def load_library(path):
 
 @dataclass(frozen=True)
 class AttentionConfig:
-    """Launch configuration: accumulation variant, tile selector (0 = automatic)
-    and capture (debug) mode, which records every row's online-softmax
+    """Launch configuration: accumulation variant, tile selector (0 = automatic),
+    capture (debug) mode, which records every row's online-softmax
     statistics per key block (the reference config's ``capture`` flag,
-    ``backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/backend.py:27``)."""
+    ``backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/backend.py:27``), and the
+    attention mask (``FA_CAUSAL``; a row that sees no key gets O = 0 and
+    lse = -inf)."""
     acc: str = "fp32"
     kernel: int = 0
     capture: bool = False
+    causal: str = "none"
 
     def __post_init__(self):
         if self.acc not in FA_ACC:
@@ -87,12 +95,15 @@ class AttentionConfig:
             raise ValueError("kernel selector must be a non-negative int")
         if not isinstance(self.capture, bool):
             raise ValueError("capture must be a bool")
+        if self.causal not in FA_CAUSAL:
+            raise ValueError(f"unknown causal mode {self.causal!r}")
 
 
 def make_problem(q_shape, k_shape, scale, config):
     b, hq, nq, d = q_shape
     _, hkv, nk, _ = k_shape
-    return FaProblem(b, hq, hkv, nq, nk, d, float(scale), FA_ACC[config.acc], config.kernel, 0)
+    return FaProblem(b, hq, hkv, nq, nk, d, float(scale), FA_ACC[config.acc], config.kernel,
+                     FA_CAUSAL[config.causal])
 
 
 class Operator:
@@ -142,6 +153,8 @@ class Operator:
         rows, keys = self.tile(q.shape, k.shape)
         if nq % rows or k.shape[2] % keys or max(nq, k.shape[2]) >= 2 ** 30:
             raise ValueError(f"unsupported query/key tail (Nq % {rows}, Nk % {keys})")
+        if self.config.causal != "none" and (rows, keys) != (1, 1):
+            raise ValueError("a causal mask needs a masking tile (kernel 0 or a ping-pong tile)")
         for t in (q, k, v):
             if t.device.type != "cuda" or t.device != q.device or t.dtype != torch.float16 \
                     or not t.is_contiguous():

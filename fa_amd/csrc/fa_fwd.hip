@@ -1,5 +1,5 @@
-// Flash-attention forward for MI355X (gfx950): non-causal GQA, D = 128,
-// FP16 in/out, FP32- or FP16-accumulated O.
+// Flash-attention forward for MI355X (gfx950): GQA, D = 128, FP16 in/out,
+// FP32- or FP16-accumulated O, full (non-causal) or causal attention.
 //
 // Work decomposition (reference: task = (batch*head, query block), KV head
 // = head / group, backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/project/
@@ -10,8 +10,9 @@
 // once in LDS (a ring of slots) and read by every wave, and every wave keeps
 // its Q fragments, O accumulators and softmax statistics in registers for the
 // whole key loop. The ping-pong body also masks ragged query and key tails,
-// writes the per-row log-sum-exp on request, and has a capture variant that
-// records the per-block softmax statistics.
+// writes the per-row log-sum-exp on request, applies an optional causal mask
+// (a query tile then streams only the key blocks up to its diagonal), and has
+// a capture variant that records the per-block softmax statistics.
 //
 // Matrix products run transposed so the softmax is lane-local:
 //   S^T = K Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS, B = Q^T
@@ -65,7 +66,9 @@ constexpr float LN2 = 0.6931471805599453f;
 // holding the running max m (natural-log units, scale * score), the running
 // sum l relative to m, the rescale factor alpha applied at that block, and
 // the block's own row sum z relative to m. c is the softmax scale times
-// log2(e).
+// log2(e). With causal set, query row i sees keys j <= i + causal_off only
+// (causal_off = 0 aligns the mask top-left, Nk - Nq bottom-right); a row that
+// sees no key gets O = 0 and lse = -inf.
 struct FaArgs {
   const _Float16* q;
   const _Float16* k;
@@ -74,6 +77,7 @@ struct FaArgs {
   float* lse;
   float* stats;
   int heads_q, group, seq_q, seq_k, nk_valid;
+  int causal, causal_off;
   float c;
 };
 
@@ -158,7 +162,7 @@ __global__ void __launch_bounds__(256) fa_prep_kernel(const _Float16* __restrict
 
 // The attention body. ACC16 selects the FP16 O accumulator; NW waves per
 // workgroup, SUB 32-row subtiles per wave, BN keys per block.
-// Requires Nq % BM == 0 and Nk % BN == 0 (no masked tail).
+// Requires Nq % BM == 0 and Nk % BN == 0 (no masked tail) and no causal mask.
 template <bool ACC16, int NW, int SUB, int BN>
 __device__ __forceinline__ void fa_fwd_body(const FaArgs& args) {
   const _Float16* __restrict__ q = args.q;
@@ -474,10 +478,22 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   const int grp = SPLIT_HI ? (wave_u >> 2) : (wave_u & 1);
 
   // Query tiles may run past Nq (a ragged last tile): its rows past the end
-  // compute on a copy of the last row and store nothing.
+  // compute on a copy of the last row and store nothing. Without a mask,
+  // consecutive workgroups walk the query tiles of one (batch, head); with the
+  // causal mask, whose tiles differ in work, they walk the heads of one query
+  // tile, the tiles with the most key blocks first, so the short tiles fill
+  // the end of the dispatch.
   const int tiles_q = (seq_q + BM - 1) / BM;
-  const int bh = blockIdx.x / tiles_q;
-  const int qt = blockIdx.x - bh * tiles_q;
+  const int nbh = gridDim.x / tiles_q;
+  int bh, qt;
+  if (args.causal) {
+    const int r = blockIdx.x / nbh;
+    bh = blockIdx.x - r * nbh;
+    qt = tiles_q - 1 - r;
+  } else {
+    bh = blockIdx.x / tiles_q;
+    qt = blockIdx.x - bh * tiles_q;
+  }
   const int b = bh / heads_q, h = bh - b * heads_q;
   const int heads_kv = heads_q / group;
   const size_t kv = (size_t)b * heads_kv + h / group;
@@ -486,6 +502,43 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   const int row = qt * BM + wave_u * 32 + l32;          // this lane's query row in (b, h)
   const bool row_ok = row < seq_q;
   const size_t grow = (size_t)bh * seq_q + (row_ok ? row : seq_q - 1);
+
+  // Last key this lane's row sees (klim) and the smallest such limit over the
+  // wave (klim_w, wave-uniform: the wave's first row); blocks past klim_w need
+  // per-element masking. With the causal mask the workgroup streams only the
+  // key blocks its last row sees.
+  int nblk = seq_k / BN;
+  int klim = nk_valid - 1, klim_w = nk_valid - 1;
+  if (args.causal) {
+    klim = min(klim, row + args.causal_off);
+    klim_w = min(klim_w, qt * BM + wave_u * 32 + args.causal_off);
+    const int kend = min(qt * BM + BM, seq_q) + args.causal_off;   // keys [0, kend) are seen
+    nblk = kend <= 0 ? 0 : min(nblk, (kend + BN - 1) / BN);
+  }
+  if (nblk == 0) {
+    // No row of this tile sees a key (bottom-right mask, Nq > Nk): O = 0 and
+    // lse = -inf. Uniform over the workgroup, before any barrier or load.
+    if constexpr (CAPTURE) {
+      if (hf == 0 && row_ok) {
+        const size_t rows = (size_t)nbh * seq_q, nb = seq_k / BN;
+        for (size_t j = 0; j < nb; ++j) {
+          args.stats[(0 * nb + j) * rows + grow] = -INFINITY;
+          args.stats[(1 * nb + j) * rows + grow] = 0.f;
+          args.stats[(2 * nb + j) * rows + grow] = 1.f;
+          args.stats[(3 * nb + j) * rows + grow] = 0.f;
+        }
+      }
+    }
+    if (!row_ok) return;
+    if (args.lse && hf == 0) args.lse[grow] = -INFINITY;
+    const h4 zero = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<h4*>(o + grow * HD + dt * 32 + 8 * g + 4 * hf) = zero;
+    return;
+  }
 
   h8 qf[8];
 #pragma unroll
@@ -627,7 +680,6 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   for (int i = tid; i < VBYTES / 16; i += NT)
     reinterpret_cast<u32x4*>(vbase + (NS - 1) * VBYTES)[i] = u32x4{0u, 0u, 0u, 0u};
 
-  const int nblk = seq_k / BN;
   const int last = nblk - 1;
   // Prologue (group 0): K(0..NS-2) -> slots 0..NS-2 and V(0..NS-3) -> slots
   // 0..NS-3, everything pairs before pair 0 would have loaded. Block indices
@@ -656,15 +708,16 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
           acc16[dt][i] = acc16[dt][i] * a2 + pv;
         }
     }
-    // Keys at or past nk_valid (zero padding of a ragged last block) score
-    // -inf: they get P = 0. S^T register r of lane half hf holds key
-    // 32t + 8(r / 4) + 4hf + r % 4 of the block.
-    if (key0 + BN > nk_valid) {
+    // Keys past the row's limit (zero padding of a ragged last block, keys
+    // beyond the causal diagonal) score -inf: they get P = 0. S^T register r
+    // of lane half hf holds key 32t + 8(r / 4) + 4hf + r % 4 of the block.
+    if (key0 + BN - 1 > klim_w) {
+      const int lim = klim - key0 - 4 * hf;
 #pragma unroll
       for (int t = 0; t < KT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          if (key0 + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3) >= nk_valid) s[t][r] = -INFINITY;
+          if (32 * t + 8 * (r >> 2) + (r & 3) > lim) s[t][r] = -INFINITY;
     }
     // Row max as a balanced 3-ary tree of v_maximum3 (independent maxima
     // issue back to back; a running max would be one long dependent chain).
@@ -722,10 +775,10 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
     if constexpr (CAPTURE) {         // capture mode: this block's row statistics
       const float z = half_sum(zsum), lrow = half_sum(lsum);
       if (hf == 0 && row_ok) {
-        const size_t rows = (size_t)gridDim.x / tiles_q * seq_q;   // B * Hq * Nq
+        const size_t rows = (size_t)nbh * seq_q;   // B * Hq * Nq
         const size_t nb = seq_k / BN, j = key0 / BN;
         float* st = args.stats + grow;
-        st[(0 * nb + j) * rows] = m * c * LN2;
+        st[(0 * nb + j) * rows] = m == NEG_BIG ? -INFINITY : m * c * LN2;
         st[(1 * nb + j) * rows] = lrow;
         st[(2 * nb + j) * rows] = alpha;
         st[(3 * nb + j) * rows] = z;
@@ -773,6 +826,20 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   // No DMA may still be writing this workgroup's LDS when it exits.
   wait_dma(0);
 
+  if constexpr (CAPTURE) {
+    // Key blocks past the causal diagonal leave every statistic unchanged.
+    const float lrow = half_sum(lsum);
+    if (hf == 0 && row_ok) {
+      const size_t rows = (size_t)nbh * seq_q, nb = seq_k / BN;
+      for (size_t j = nblk; j < nb; ++j) {
+        args.stats[(0 * nb + j) * rows + grow] = m == NEG_BIG ? -INFINITY : m * c * LN2;
+        args.stats[(1 * nb + j) * rows + grow] = lrow;
+        args.stats[(2 * nb + j) * rows + grow] = 1.f;
+        args.stats[(3 * nb + j) * rows + grow] = 0.f;
+      }
+    }
+  }
+
   if constexpr (ACC16) {
     // The last block's PV (computed in the final MFMA step) is still pending.
     const _Float16 a16 = (_Float16)alpha_prev;
@@ -787,9 +854,10 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   }
 
   // Epilogue: O / l -> FP16 and the row's log-sum-exp
-  // ln(l) + scale * m = (log2(l) + c * m) * ln 2, for rows inside Nq.
+  // ln(l) + scale * m = (log2(l) + c * m) * ln 2, for rows inside Nq. A row
+  // that saw no key (causal mask) has l = 0: O = 0 and lse = -inf.
   const float l = half_sum(lsum);
-  const float inv = 1.f / l;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
   if (!row_ok) return;
   if (args.lse && hf == 0) args.lse[grow] = (__builtin_amdgcn_logf(l) + m * c) * LN2;
   _Float16* orow = o + grow * HD;
@@ -853,7 +921,7 @@ struct TileConfig {
   int rows;        // BM
   int keys;        // BN
   int lds;         // dynamic LDS bytes per workgroup
-  bool tails;      // masks ragged query and key tails (any Nq, Nk); has capture mode
+  bool tails;      // masks ragged query and key tails (any Nq, Nk) and causal masks; has capture mode
   attn_fn fp32;
   attn_fn fp16;
   attn_fn fp32_capture;   // null when the tile has no capture mode
@@ -890,6 +958,7 @@ static_assert(sizeof(kAutoOrderFp32) == sizeof(int) * kNumTiles &&
               "every tile appears in each automatic order");
 
 bool tile_fits(const TileConfig& t, const fa_problem* p) {
+  if (p->causal != FA_CAUSAL_NONE) return t.tails;
   return t.tails || (p->seq_q > 0 && p->seq_k > 0 && p->seq_q % t.rows == 0 && p->seq_k % t.keys == 0);
 }
 
@@ -940,9 +1009,12 @@ int validate(const fa_problem* p, const TileConfig** tile) {
   if (p->dim != HD) return FA_ERR_DIM;
   if (p->acc != FA_ACC_FP32 && p->acc != FA_ACC_FP16) return FA_ERR_ACC;
   if (!(p->scale > 0.f) || !isfinite(p->scale)) return FA_ERR_SCALE;
-  if (p->reserved != 0) return FA_ERR_KERNEL;
+  if (p->causal != FA_CAUSAL_NONE && p->causal != FA_CAUSAL_TOP_LEFT &&
+      p->causal != FA_CAUSAL_BOTTOM_RIGHT)
+    return FA_ERR_CAUSAL;
   int rc = select_tile(p, tile);
   if (rc) return rc;
+  if (p->causal != FA_CAUSAL_NONE && !(*tile)->tails) return FA_ERR_CAUSAL;
   // 32-bit index limits used inside the kernels (the padded key length too).
   const int64_t lim = (int64_t)1 << 30;
   if (p->seq_q >= lim || p->seq_k >= lim - 128 || p->heads_q >= lim || p->batch >= lim)
@@ -998,6 +1070,8 @@ int launch(const fa_problem* p, const void* q, const void* k, const void* v, voi
   args.seq_q = (int)p->seq_q;
   args.seq_k = (int)lay.nk_pad;
   args.nk_valid = (int)p->seq_k;
+  args.causal = p->causal != FA_CAUSAL_NONE;
+  args.causal_off = p->causal == FA_CAUSAL_BOTTOM_RIGHT ? (int)(p->seq_k - p->seq_q) : 0;
   args.c = (float)((double)p->scale * LOG2E);
   const int64_t tiles_q = (p->seq_q + tile->rows - 1) / tile->rows;
   const unsigned grid = (unsigned)(p->batch * p->heads_q * tiles_q);
@@ -1094,6 +1168,7 @@ const char* fa_strerror(int status) {
     case FA_ERR_KERNEL: return "unknown kernel selector";
     case FA_ERR_LAUNCH: return "HIP kernel launch failed";
     case FA_ERR_CAPTURE: return "capture needs a ping-pong tile and a stats buffer of fa_fwd_capture_count() floats";
+    case FA_ERR_CAUSAL: return "unknown causal mode, or a causal mask asked of a tile without masking";
     default: return "unknown status";
   }
 }

@@ -1,13 +1,17 @@
 /*
  * fa_hip.h -- C ABI of libfa_hip.so, the MI355X (gfx950) flash-attention
- * forward for non-causal grouped-query attention, FP16 in and FP16 out.
+ * forward for grouped-query attention, FP16 in and FP16 out, full
+ * (non-causal, the reference's only mode) or causal.
  *
  * Layout: q [B, Hq, Nq, 128], k and v [B, Hkv, Nk, 128], o [B, Hq, Nq, 128],
  * all contiguous FP16 in device memory. Output rows are the normalised
  * softmax(q k^T * scale) v with query head h reading key/value head
  * h / (Hq / Hkv). Any Nq, Nk >= 1 with the automatic tile choice (ragged
  * query and key tails are masked); fa_fwd_lse() also returns the per-row
- * log-sum-exp.
+ * log-sum-exp. With fa_problem.causal set, query row i attends only to keys
+ * j <= i (top-left, torch's scaled_dot_product_attention(is_causal=True)) or
+ * j <= i + Nk - Nq (bottom-right); a row that sees no key gets O = 0 and
+ * lse = -inf.
  *
  * Conventions (mirroring the reference's two-phase operator binding):
  *   - every entry point returns 0 on success and a nonzero FA_ERR_* code
@@ -42,12 +46,22 @@ enum fa_status {
   FA_ERR_SCALE = 8,         /* scale not finite and positive */
   FA_ERR_KERNEL = 9,        /* unknown kernel selector */
   FA_ERR_LAUNCH = 10,       /* the HIP runtime rejected a launch */
-  FA_ERR_CAPTURE = 11       /* capture asked of a tile without it, or stats buffer too small */
+  FA_ERR_CAPTURE = 11,      /* capture asked of a tile without it, or stats buffer too small */
+  FA_ERR_CAUSAL = 12        /* unknown causal mode, or a causal mask asked of a tile without masking */
 };
 
 enum fa_acc {
   FA_ACC_FP32 = 0,          /* O accumulated in FP32 registers across all keys */
   FA_ACC_FP16 = 1           /* per-block PV rounded to FP16, O accumulated in FP16 */
+};
+
+/* Attention mask. The reference runs full attention only (sparse_mode=0 in
+ * backends/npu_fa/backend.py:48, is_causal=False in
+ * backends/expert_v2/impl.py:714); the causal modes are additions. */
+enum fa_causal {
+  FA_CAUSAL_NONE = 0,         /* every query row sees every key */
+  FA_CAUSAL_TOP_LEFT = 1,     /* row i sees keys j <= i */
+  FA_CAUSAL_BOTTOM_RIGHT = 2  /* row i sees keys j <= i + Nk - Nq */
 };
 
 typedef struct fa_problem {
@@ -60,7 +74,7 @@ typedef struct fa_problem {
   float scale;              /* softmax scale, normally dim ** -0.5 */
   int32_t acc;              /* enum fa_acc */
   int32_t kernel;           /* 0 = automatic tile choice; k >= 1 forces tile configuration k */
-  int32_t reserved;         /* must be 0 */
+  int32_t causal;           /* enum fa_causal (0 = full attention) */
 } fa_problem;
 
 /*

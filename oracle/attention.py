@@ -48,6 +48,19 @@ Functions and what pins each (tests/test_oracle.py):
                        K32/vector_output.h:22-38); pinned by the last prefix
                        equalling lse_f64, each block equalling lse_f64 of its
                        key slice, and the logaddexp recursion of the prefixes.
+  causal masks         every function above takes ``causal`` ("none",
+                       "top_left": key j <= i, "bottom_right": j <= i + Nk -
+                       Nq; a row that sees no key has O = 0, lse = -inf). The
+                       reference runs full attention only (sparse_mode=0,
+                       backends/npu_fa/backend.py:48; is_causal=False,
+                       backends/expert_v2/impl.py:714), so the masks are
+                       additions, pinned against torch's float64
+                       scaled_dot_product_attention (is_causal=True for
+                       top-left, an explicit boolean mask for bottom-right),
+                       the closed form O[row 0] = v[key 0] (top-left), prefix
+                       consistency (row i equals full attention over keys
+                       0..i) and bottom-right's last row equalling full
+                       attention.
 Every check above plants a mistake in the oracle (dropped scale, swapped GQA
 map, transposed operand) and confirms at least one check fails
 (tests/test_oracle.py::test_checks_catch_planted_mistakes).
@@ -67,8 +80,37 @@ def _scale(d, scale):
     return float(d) ** -0.5 if scale is None else float(scale)
 
 
-def attention_loops(q, k, v, scale=None):
-    """Definition by loops: o[b,h,i] = sum_j softmax_j(q.k_j * scale) v_j.
+CAUSAL_MODES = ("none", "top_left", "bottom_right")
+
+
+def key_limit(rows, nq, nk, causal="none"):
+    """Index of the last key each query row in ``rows`` sees (-1: no key).
+
+    ``none`` sees all Nk keys; ``top_left`` keys j <= i (torch's
+    scaled_dot_product_attention with is_causal=True); ``bottom_right`` keys
+    j <= i + Nk - Nq (the last query row sees every key).
+    """
+    rows = np.asarray(rows, dtype=np.int64)
+    if causal == "none":
+        return np.full(rows.shape, nk - 1, dtype=np.int64)
+    if causal == "top_left":
+        return np.minimum(nk - 1, rows)
+    if causal == "bottom_right":
+        return np.clip(rows + (nk - nq), -1, nk - 1)
+    raise ValueError(f"unknown causal mode {causal!r}")
+
+
+def _mask(s, lim):
+    """Scores ``s`` [rows, Nk] with keys past each row's limit set to -inf."""
+    if lim is None:
+        return s
+    j = np.arange(s.shape[-1])
+    return np.where(j[None, :] > np.asarray(lim)[:, None], -np.inf, s)
+
+
+def attention_loops(q, k, v, scale=None, causal="none"):
+    """Definition by loops: o[b,h,i] = sum_j softmax_j(q.k_j * scale) v_j over
+    the keys row i sees (all, or those up to ``key_limit``).
 
     Intended for tiny shapes only (pure Python).
     """
@@ -84,8 +126,11 @@ def attention_loops(q, k, v, scale=None):
         for h in range(hq):
             hk = h // group
             for i in range(nq):
+                last = int(key_limit([i], nq, nk, causal)[0])
+                if last < 0:
+                    continue                     # no key: O = 0
                 logits = []
-                for j in range(nk):
+                for j in range(last + 1):
                     dot = 0.0
                     for x in range(d):
                         dot += q[b, h, i, x] * k[b, hk, j, x]
@@ -95,20 +140,24 @@ def attention_loops(q, k, v, scale=None):
                 z = sum(w)
                 for x in range(d):
                     acc = 0.0
-                    for j in range(nk):
+                    for j in range(last + 1):
                         acc += w[j] * v[b, hk, j, x]
                     out[b, h, i, x] = acc / z
     return out
 
 
 def _softmax_rows_f64(s):
-    s = s - s.max(axis=-1, keepdims=True)
+    """Row softmax; a row of only -inf (no visible key) becomes zeros."""
+    mx = s.max(axis=-1, keepdims=True)
+    empty = ~np.isfinite(mx)
+    s = s - np.where(empty, 0.0, mx)
     np.exp(s, out=s)
-    s /= s.sum(axis=-1, keepdims=True)
+    z = s.sum(axis=-1, keepdims=True)
+    s /= np.where(empty, 1.0, z)
     return s
 
 
-def attention_f64(q, k, v, scale=None, chunk_rows=1024):
+def attention_f64(q, k, v, scale=None, chunk_rows=1024, causal="none"):
     """Exact-as-float64 attention over [B,H,N,D]; returns float64 [B,Hq,Nq,D]."""
     q, k, v = (_np(t) for t in (q, k, v))
     b_, hq, nq, d = q.shape
@@ -124,12 +173,14 @@ def attention_f64(q, k, v, scale=None, chunk_rows=1024):
             vf = v[b, h // group].astype(np.float64)
             for r0 in range(0, nq, chunk_rows):
                 qf = q[b, h, r0:r0 + chunk_rows].astype(np.float64)
-                p = _softmax_rows_f64((qf @ kf.T) * sc)
+                lim = None if causal == "none" else \
+                    key_limit(np.arange(r0, r0 + len(qf)), nq, nk, causal)
+                p = _softmax_rows_f64(_mask((qf @ kf.T) * sc, lim))
                 out[b, h, r0:r0 + chunk_rows] = p @ vf
     return out
 
 
-def attention_rows_f64(q, k, v, rows, scale=None):
+def attention_rows_f64(q, k, v, rows, scale=None, causal="none"):
     """float64 output rows for ``rows = [(b, h, i), ...]``; returns [len(rows), D].
 
     Every output row depends only on its own query row and the full K/V of
@@ -137,7 +188,7 @@ def attention_rows_f64(q, k, v, rows, scale=None):
     references for the corresponding rows of a full GPU result.
     """
     q, k, v = (_np(t) for t in (q, k, v))
-    hq, d = q.shape[1], q.shape[3]
+    hq, nq, d = q.shape[1], q.shape[2], q.shape[3]
     group = hq // k.shape[1]
     sc = _scale(d, scale)
     out = np.empty((len(rows), d), dtype=np.float64)
@@ -148,7 +199,9 @@ def attention_rows_f64(q, k, v, rows, scale=None):
         kf = k[b, hk].astype(np.float64)
         vf = v[b, hk].astype(np.float64)
         qf = np.stack([q[b, h, i].astype(np.float64) for _, h, i in items])
-        p = _softmax_rows_f64((qf @ kf.T) * sc)
+        lim = None if causal == "none" else \
+            key_limit([i for _, _, i in items], nq, kf.shape[0], causal)
+        p = _softmax_rows_f64(_mask((qf @ kf.T) * sc, lim))
         res = p @ vf
         for m, (n, _, _) in enumerate(items):
             out[n] = res[m]
@@ -156,41 +209,49 @@ def attention_rows_f64(q, k, v, rows, scale=None):
 
 
 def _lse_rows(s):
-    """ln sum exp over the last axis of float64 scores, max-shifted."""
+    """ln sum exp over the last axis of float64 scores, max-shifted (-inf for
+    a row of only -inf)."""
     mx = s.max(axis=-1)
-    return mx + np.log(np.exp(s - mx[..., None]).sum(axis=-1))
+    safe = np.where(np.isfinite(mx), mx, 0.0)
+    with np.errstate(divide="ignore"):
+        return safe + np.log(np.exp(s - safe[..., None]).sum(axis=-1))
 
 
-def lse_f64(q, k, scale=None, chunk_rows=1024):
+def lse_f64(q, k, scale=None, chunk_rows=1024, causal="none"):
     """float64 [B, Hq, Nq]: lse[b,h,i] = ln sum_j exp(scale * q[b,h,i] . k[b,h//g,j])."""
     q, k = _np(q), _np(k)
     b_, hq, nq, d = q.shape
     group = hq // k.shape[1]
     sc = _scale(d, scale)
+    nk = k.shape[2]
     out = np.empty((b_, hq, nq), dtype=np.float64)
     for b in range(b_):
         for h in range(hq):
             kf = k[b, h // group].astype(np.float64)
             for r0 in range(0, nq, chunk_rows):
                 qf = q[b, h, r0:r0 + chunk_rows].astype(np.float64)
-                out[b, h, r0:r0 + chunk_rows] = _lse_rows((qf @ kf.T) * sc)
+                lim = None if causal == "none" else \
+                    key_limit(np.arange(r0, r0 + len(qf)), nq, nk, causal)
+                out[b, h, r0:r0 + chunk_rows] = _lse_rows(_mask((qf @ kf.T) * sc, lim))
     return out
 
 
-def lse_rows_f64(q, k, rows, scale=None):
+def lse_rows_f64(q, k, rows, scale=None, causal="none"):
     """float64 log-sum-exp for ``rows = [(b, h, i), ...]`` (rows are independent)."""
     q, k = _np(q), _np(k)
-    hq, d = q.shape[1], q.shape[3]
+    hq, nq, d = q.shape[1], q.shape[2], q.shape[3]
     group = hq // k.shape[1]
+    nk = k.shape[2]
     sc = _scale(d, scale)
     out = np.empty(len(rows), dtype=np.float64)
     for n, (b, h, i) in enumerate(rows):
         s = (k[b, h // group].astype(np.float64) @ q[b, h, i].astype(np.float64)) * sc
+        s = _mask(s[None, :], key_limit([i], nq, nk, causal))[0]
         out[n] = _lse_rows(s)
     return out
 
 
-def block_stats_f64(q, k, block, scale=None):
+def block_stats_f64(q, k, block, scale=None, causal="none"):
     """Exact statistics per key block of ``block`` keys (the last may be ragged).
 
     Returns float64 arrays of shape [nblk, B, Hq, Nq]:
@@ -206,9 +267,11 @@ def block_stats_f64(q, k, block, scale=None):
     sc = _scale(d, scale)
     nblk = -(-nk // block)
     out = {n: np.empty((nblk, b_, hq, nq)) for n in ("lse_prefix", "lse_block", "max_prefix", "max_block")}
+    lim = None if causal == "none" else key_limit(np.arange(nq), nq, nk, causal)
     for b in range(b_):
         for h in range(hq):
             s = (q[b, h].astype(np.float64) @ k[b, h // group].astype(np.float64).T) * sc
+            s = _mask(s, lim)
             for n in range(nblk):
                 blk = s[:, n * block:(n + 1) * block]
                 pre = s[:, :(n + 1) * block]

@@ -62,8 +62,14 @@ def check(out, exact, acc, what):
 
 
 def check_lse(lse, exact, what):
-    err = np.abs(lse.astype(np.float64) - exact)
-    worst = float(err.max())
+    """lse within LSE_ATOL + LSE_RTOL |exact|; rows that see no key (exact
+    -inf, causal masks only) must be exactly -inf."""
+    lse = lse.astype(np.float64)
+    none = np.isneginf(exact)
+    assert bool(np.all(np.isneginf(lse[none]))), f"{what}: lse of a row without keys is not -inf"
+    lse, exact = lse[~none], exact[~none]
+    err = np.abs(lse - exact)
+    worst = float(err.max()) if err.size else 0.0
     say(f"  {what} lse max_abs={worst:.3e}")
     assert bool(np.all(np.isfinite(lse))), f"{what}: non-finite lse"
     within = bool(np.all(err <= LSE_ATOL + LSE_RTOL * np.abs(exact)))
@@ -362,3 +368,137 @@ def test_golden_fixture(ops):
     dev = {n: torch.from_numpy(data[n]).cuda() for n in ("q", "k", "v")}
     for acc, op in ops.items():
         check(run(op, dev), data["out"].astype(np.float64), acc, "golden")
+
+
+# --------------------------------------------------------------------------- #
+# causal masks
+# --------------------------------------------------------------------------- #
+# (B, Hq, Hkv, Nq, Nk, sigma): square, ragged, Nq < Nk, Nq > Nk (bottom-right
+# leaves its first Nq - Nk rows without keys), single row, wide logits.
+CAUSAL = [(1, 12, 1, 256, 256, 1.0), (1, 4, 2, 1000, 1000, 1.0), (2, 4, 1, 300, 1100, 1.0),
+          (1, 4, 1, 1100, 300, 1.0), (1, 2, 1, 1, 1, 1.0), (1, 3, 1, 257, 129, 1.0),
+          (1, 2, 1, 700, 700, 3.0)]
+
+
+def causal_inputs(b, hq, hkv, nq, nk, sig, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(b, hq, nq, 128, generator=g) * sig).half()
+    k = (torch.randn(b, hkv, nk, 128, generator=g) * sig).half()
+    v = torch.randn(b, hkv, nk, 128, generator=g).half()
+    if sig > 1:
+        v[:, :, ::23] *= 8
+    return q, k, v
+
+
+@pytest.mark.parametrize("acc", ["fp32", "fp16"])
+@pytest.mark.parametrize("causal", ["top_left", "bottom_right"])
+@pytest.mark.parametrize("b,hq,hkv,nq,nk,sig", CAUSAL)
+def test_causal_vs_f64(library_path, b, hq, hkv, nq, nk, sig, causal, acc):
+    say(f"case causal={causal} B{b} Hq{hq} Hkv{hkv} nq={nq} nk={nk} sig={sig} acc={acc}")
+    q, k, v = causal_inputs(b, hq, hkv, nq, nk, sig, seed=nq * 13 + nk)
+    op = Operator(library_path, AttentionConfig(acc=acc, causal=causal))
+    assert op.kernel_name(q.shape, k.shape).startswith("pp_")
+    out, lse = op(q.cuda(), k.cuda(), v.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    out = out.float().cpu().numpy()
+    check(out, orc.attention_f64(q, k, v, causal=causal), acc, "causal")
+    exact_lse = orc.lse_f64(q, k, causal=causal)
+    check_lse(lse.cpu().numpy(), exact_lse, "causal")
+    empty = np.isneginf(exact_lse)
+    assert bool(np.all(out[empty] == 0)), "rows without keys must be exactly zero"
+
+
+@pytest.mark.parametrize("kernel", [k for k in kernel_ids() if kernel_name(k).startswith("pp_")]
+                         if kernel_ids() != [1] else [])
+def test_causal_every_masking_tile(library_path, kernel):
+    nq, nk = 600, 900
+    say(f"case causal tile {kernel} nq={nq} nk={nk}")
+    q, k, v = causal_inputs(2, 6, 2, nq, nk, 1.0, seed=kernel)
+    dev = [t.cuda() for t in (q, k, v)]
+    for causal in ("top_left", "bottom_right"):
+        exact = orc.attention_f64(q, k, v, causal=causal)
+        for acc in ("fp32", "fp16"):
+            op = Operator(library_path, AttentionConfig(acc=acc, kernel=kernel, causal=causal))
+            check(run(op, {"q": dev[0], "k": dev[1], "v": dev[2]}), exact, acc,
+                  f"causal {causal} tile{kernel}")
+
+
+def test_causal_none_unchanged_and_repeatable(library_path):
+    """causal="none" is the full-attention kernel (bitwise), and a causal
+    result is the same on every call."""
+    say("case causal none/repeat nq=nk=1024")
+    q, k, v = causal_inputs(1, 4, 1, 1024, 1024, 1.0, seed=4)
+    dev = [t.cuda() for t in (q, k, v)]
+    full = Operator(library_path, AttentionConfig())(*dev).clone()
+    none = Operator(library_path, AttentionConfig(causal="none"))(*dev).clone()
+    op = Operator(library_path, AttentionConfig(causal="top_left"))
+    a = op(*dev).clone()
+    b = op(*dev).clone()
+    torch.cuda.synchronize()
+    assert bool(torch.equal(full, none))
+    assert bool(torch.equal(a, b))
+    # The last row sees every key under both masks when Nq = Nk.
+    assert float((a[:, :, -1].float() - full[:, :, -1].float()).abs().max()) <= 1e-3
+
+
+def _close_or_both_neginf(a, b, tol):
+    both = np.isneginf(a) & np.isneginf(b)
+    return bool(np.all(both | (np.abs(np.where(both, 0, a) - np.where(both, 0, b)) <= tol)))
+
+
+@pytest.mark.parametrize("acc", ["fp32", "fp16"])
+@pytest.mark.parametrize("causal,nq,nk", [("top_left", 300, 700), ("bottom_right", 500, 200),
+                                          ("top_left", 1000, 300)])
+def test_causal_capture_statistics(library_path, causal, nq, nk, acc):
+    """Capture mode under a causal mask: per-block m, l, alpha, z against the
+    exact masked block statistics (blocks past a row's diagonal add nothing)."""
+    say(f"case causal capture {causal} nq={nq} nk={nk} acc={acc}")
+    q, k, v = causal_inputs(1, 2, 1, nq, nk, 2.0, seed=nq + nk)
+    op = Operator(library_path, AttentionConfig(acc=acc, capture=True, causal=causal))
+    out, lse = op(q.cuda(), k.cuda(), v.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    m, l, alpha, z = (t.double().cpu().numpy() for t in op.last["stats"])
+    ex = orc.block_stats_f64(q, k, op.last["block_keys"], causal=causal)
+    check(out.float().cpu().numpy(), orc.attention_f64(q, k, v, causal=causal), acc, "capture O")
+    with np.errstate(divide="ignore", invalid="ignore"):
+        total = m + np.log(l)
+        assert _close_or_both_neginf(total, ex["lse_prefix"], LSE_ATOL)
+        zx = np.exp(ex["lse_block"] - np.where(np.isneginf(m), 0, m))
+    zx[np.isneginf(ex["lse_block"])] = 0
+    assert bool(np.all(np.abs(z - zx) <= LSE_ATOL * zx + op.last["block_keys"] * 2.0 ** -24))
+    seen = np.isfinite(m[:-1])
+    assert bool(np.all(alpha[1:][~seen] == 1))
+    assert bool(np.allclose(alpha[1:][seen], np.exp(m[:-1][seen] - m[1:][seen]), rtol=1e-5))
+    assert bool(np.allclose(l[1:], alpha[1:] * l[:-1] + z[1:], rtol=1e-5, atol=0))
+    assert bool(np.all(np.isneginf(m) == np.isneginf(ex["max_prefix"])))
+    fin = np.isfinite(m)
+    tol = 1e-4 * np.abs(ex["max_prefix"][fin]) + 1e-4
+    lag = 0.0 if acc == "fp16" else 8 * np.log(2)
+    assert bool(np.all(m[fin] <= ex["max_prefix"][fin] + tol))
+    assert bool(np.all(ex["max_prefix"][fin] - m[fin] <= lag + tol))
+
+
+CAUSAL_FULL = [(1, "fp32", "top_left"), (2, "fp32", "bottom_right"), (2, "fp16", "top_left")]
+
+
+@pytest.mark.parametrize("idx,acc,causal", CAUSAL_FULL,
+                         ids=[f"c{i}-{a}-{c}" for i, a, c in CAUSAL_FULL])
+def test_causal_full_size_sampled_rows(library_path, idx, acc, causal):
+    case = CASES[idx]
+    say(f"case causal c{idx} {case.name} acc={acc} causal={causal}: generating inputs")
+    cpu, dev = inputs(case)
+    say(f"case causal c{idx} {case.name} acc={acc} causal={causal}: launching")
+    op = Operator(library_path, AttentionConfig(acc=acc, causal=causal))
+    out, lse = op(dev["q"], dev["k"], dev["v"], return_lse=True)
+    torch.cuda.synchronize()
+    rows = orc.sample_rows(cpu["q"].shape, 96, seed=idx + 10)
+    idx_t = torch.tensor(rows)
+    got = out[idx_t[:, 0], idx_t[:, 1], idx_t[:, 2]].float().cpu().numpy()
+    assert bool(np.all(np.isfinite(out.float().abs().amax(dim=(2, 3)).cpu().numpy())))
+    exact = orc.attention_rows_f64(cpu["q"], cpu["k"], cpu["v"], rows, causal=causal)
+    check(got, exact, acc, f"causal c{idx} sampled rows")
+    got_lse = lse[idx_t[:, 0], idx_t[:, 1], idx_t[:, 2]].cpu().numpy()
+    check_lse(got_lse, orc.lse_rows_f64(cpu["q"], cpu["k"], rows, causal=causal),
+              f"causal c{idx} sampled rows")
+    del dev, out
+    torch.cuda.empty_cache()

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol(library_path):
 
 def problem(**kw):
     base = dict(batch=1, heads_q=12, heads_kv=1, seq_q=4096, seq_k=4096, dim=128,
-                scale=128 ** -0.5, acc=0, kernel=0, reserved=0)
+                scale=128 ** -0.5, acc=0, kernel=0, causal=0)
     base.update(kw)
     return binding.FaProblem(**base)
 
@@ -60,7 +60,8 @@ def test_workspace_size(lib):
     (dict(batch=0), 2), (dict(heads_q=12, heads_kv=5), 2), (dict(seq_k=-64), 2),
     (dict(dim=64), 3), (dict(seq_q=4000, kernel=1), 4), (dict(seq_k=4100, kernel=2), 4),
     (dict(acc=2), 7), (dict(scale=0.0), 8), (dict(scale=float("inf")), 8),
-    (dict(kernel=99), 9), (dict(reserved=1), 9), (dict(seq_q=1 << 30), 2),
+    (dict(kernel=99), 9), (dict(causal=3), 12), (dict(causal=-1), 12), (dict(seq_q=1 << 30), 2),
+    (dict(causal=1, kernel=1), 12), (dict(causal=2, kernel=2), 12),
 ])
 def test_geometry_errors(lib, kw, code):
     rc, _ = ws_bytes(lib, problem(**kw))
@@ -87,6 +88,26 @@ def test_ragged_tails_and_workspace(lib):
     rows, keys = C.c_int32(), C.c_int32()
     assert lib.fa_fwd_tile(C.byref(problem()), C.byref(rows), C.byref(keys)) == 0
     assert (rows.value, keys.value) == (1, 1)
+
+
+def test_causal_selection(lib):
+    # Causal masks run on the masking (ping-pong) tiles only: the automatic
+    # choice picks one whatever the shape, explicit plain tiles are refused.
+    for causal in (1, 2):
+        for nq, nk in ((4096, 4096), (300, 1000), (1000, 7)):
+            for acc in (0, 1):
+                prob = problem(seq_q=nq, seq_k=nk, causal=causal, acc=acc)
+                idx = C.c_int32()
+                assert lib.fa_fwd_select(C.byref(prob), C.byref(idx)) == 0
+                assert lib.fa_kernel_name(idx.value).startswith(b"pp_"), (causal, nq, nk, acc)
+                assert ws_bytes(lib, prob)[0] == 0
+        for kernel in (3, 4, 5):
+            assert ws_bytes(lib, problem(causal=causal, kernel=kernel))[0] == 0
+    assert b"causal" in lib.fa_strerror(12)
+    with pytest.raises(ValueError):
+        binding.AttentionConfig(causal="diagonal")
+    assert binding.make_problem((1, 2, 8, 128), (1, 1, 8, 128), 1.0,
+                                binding.AttentionConfig(causal="bottom_right")).causal == 2
 
 
 def test_key_length_limit(lib):

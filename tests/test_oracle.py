@@ -271,3 +271,133 @@ def test_block_stats_catch_planted_mistakes():
     swapped["lse_prefix"], swapped["lse_block"] = good["lse_block"], good["lse_prefix"]
     for bad in (shifted, no_scale, swapped):
         assert not block_checks(bad, q, k, 64)
+
+
+# --------------------------------------------------------------------------- #
+# causal masks (additions beyond the reference's full attention)
+# --------------------------------------------------------------------------- #
+def sdpa_causal_f64(q, k, v, causal):
+    """torch float64 SDPA under a causal mode: is_causal=True (top-left), or an
+    explicit boolean mask tril(diagonal=Nk-Nq) (bottom-right). Rows with no
+    visible key come back NaN from torch; they are reported as zeros."""
+    qt, kt, vt = (torch.from_numpy(np.asarray(t, dtype=np.float64)) for t in (q, k, v))
+    g = qt.shape[1] // kt.shape[1]
+    kt, vt = kt.repeat_interleave(g, dim=1), vt.repeat_interleave(g, dim=1)
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    if causal == "top_left":
+        out = sdpa(qt, kt, vt, is_causal=True)
+    else:
+        nq, nk = q.shape[2], k.shape[2]
+        mask = torch.ones(nq, nk, dtype=torch.bool).tril(diagonal=nk - nq)
+        out = sdpa(qt, kt, vt, attn_mask=mask)
+    return np.nan_to_num(out.numpy(), nan=0.0)
+
+
+def causal_checks(attn, q, k, v, causal):
+    """True when ``attn(q, k, v)`` passes every pinning check of a causal mode."""
+    nq, nk = q.shape[2], k.shape[2]
+    group = q.shape[1] // k.shape[1]
+    got = attn(q, k, v)
+    ok = np.allclose(got, sdpa_causal_f64(q, k, v, causal), rtol=1e-10, atol=1e-12)
+    # Prefix consistency: row i is full attention over the keys it sees.
+    for i in sorted({0, nq // 2, nq - 1}):
+        last = i if causal == "top_left" else i + nk - nq
+        last = min(last, nk - 1)
+        if last < 0:
+            ok &= bool(np.all(got[:, :, i] == 0))
+            continue
+        full = orc.attention_f64(q[:, :, i:i + 1], k[:, :, :last + 1], v[:, :, :last + 1])
+        ok &= np.allclose(got[:, :, i:i + 1], full, rtol=1e-10, atol=1e-12)
+    if causal == "top_left":        # row 0 sees key 0 only
+        ok &= np.allclose(got[:, :, 0], np.repeat(v[:, :, 0], group, axis=1).astype(np.float64))
+    else:                           # the last row sees every key
+        ok &= np.allclose(got[:, :, -1], orc.attention_f64(q, k, v)[:, :, -1], rtol=1e-10)
+    return bool(ok)
+
+
+CAUSAL_SHAPES = [(1, 4, 2, 9, 9, 16), (1, 2, 1, 5, 12, 16), (2, 2, 1, 12, 5, 16)]
+
+
+@pytest.mark.parametrize("shape", CAUSAL_SHAPES)
+@pytest.mark.parametrize("causal", ["top_left", "bottom_right"])
+def test_causal_f64(shape, causal):
+    q, k, v = rand_qkv(*shape, seed=sum(shape))
+    assert causal_checks(lambda q, k, v: orc.attention_f64(q, k, v, causal=causal), q, k, v, causal)
+    assert np.allclose(orc.attention_loops(q, k, v, causal=causal),
+                       orc.attention_f64(q, k, v, causal=causal), rtol=1e-10, atol=1e-12)
+    rows = orc.sample_rows(q.shape, 7, seed=3)
+    full = orc.attention_f64(q, k, v, causal=causal)
+    assert np.allclose(orc.attention_rows_f64(q, k, v, rows, causal=causal),
+                       np.stack([full[b, h, i] for b, h, i in rows]), rtol=0, atol=1e-12)
+
+
+def test_causal_modes_agree_on_square_and_none_is_full():
+    q, k, v = rand_qkv(1, 2, 1, 10, 10, 16, seed=8)
+    assert np.array_equal(orc.attention_f64(q, k, v, causal="top_left"),
+                          orc.attention_f64(q, k, v, causal="bottom_right"))
+    assert np.array_equal(orc.attention_f64(q, k, v, causal="none"), orc.attention_f64(q, k, v))
+    assert list(orc.key_limit([0, 3, 9], 10, 4, "bottom_right")) == [-1, -1, 3]
+    assert list(orc.key_limit([0, 3, 9], 4, 10, "bottom_right")) == [6, 9, 9]
+    with pytest.raises(ValueError):
+        orc.key_limit([0], 4, 4, "diagonal")
+
+
+def _masked_f64(q, k, v, limit):
+    """Attention with an arbitrary per-row last-key function (planted mistakes)."""
+    nq, nk, d = q.shape[2], k.shape[2], q.shape[3]
+    group = q.shape[1] // k.shape[1]
+    out = np.zeros(q.shape)
+    for b in range(q.shape[0]):
+        for h in range(q.shape[1]):
+            s = q[b, h].astype(np.float64) @ k[b, h // group].astype(np.float64).T * d ** -0.5
+            lim = np.array([limit(i, nq, nk) for i in range(nq)])
+            out[b, h] = orc._softmax_rows_f64(orc._mask(s, lim)) @ v[b, h // group].astype(np.float64)
+    return out
+
+
+def test_causal_checks_catch_planted_mistakes():
+    q, k, v = rand_qkv(1, 2, 1, 8, 11, 16, seed=13)
+    plants = {
+        "top_left": [lambda i, nq, nk: i - 1,                  # strict: j < i
+                     lambda i, nq, nk: nk - 1,                 # mask ignored
+                     lambda i, nq, nk: min(nk - 1, i + nk - nq)],   # bottom-right instead
+        "bottom_right": [lambda i, nq, nk: min(nk - 1, i),     # top-left instead
+                         lambda i, nq, nk: min(nk - 1, i + nk - nq - 1),   # off by one
+                         lambda i, nq, nk: nk - 1 if i % 2 else min(nk - 1, i + nk - nq)],
+    }
+    for causal, bads in plants.items():
+        assert causal_checks(lambda q, k, v: orc.attention_f64(q, k, v, causal=causal), q, k, v, causal)
+        for bad in bads:
+            assert not causal_checks(lambda q, k, v: _masked_f64(q, k, v, bad), q, k, v, causal)
+
+
+@pytest.mark.parametrize("causal", ["top_left", "bottom_right"])
+def test_causal_lse_and_block_stats(causal):
+    q, k, v = rand_qkv(1, 2, 1, 12, 7, 16, seed=17)
+    nq, nk = 12, 7
+    lse = orc.lse_f64(q, k, causal=causal)
+    lim = orc.key_limit(np.arange(nq), nq, nk, causal)
+    # torch.logsumexp over the masked float64 scores; no visible key -> -inf.
+    s = torch.from_numpy(np.einsum("bhid,bjd->bhij", q.astype(np.float64),
+                                   k[:, 0].astype(np.float64)) * 16 ** -0.5)
+    s = s.masked_fill(torch.arange(nk)[None, :] > torch.from_numpy(lim)[:, None], float("-inf"))
+    assert np.allclose(lse, torch.logsumexp(s, dim=-1).numpy(), rtol=0, atol=1e-12)
+    assert np.all(np.isneginf(lse[:, :, lim < 0]))
+    # Softmax identity on the rows that see a key.
+    o = orc.attention_f64(q, k, v, causal=causal)
+    with np.errstate(invalid="ignore"):          # -inf - -inf on rows with no key
+        w = np.exp(s.numpy() - lse[..., None])
+    w[:, :, lim < 0] = 0
+    assert np.allclose(o, np.einsum("bhij,bjd->bhid", w, v[:, 0].astype(np.float64)), atol=1e-12)
+    rows = orc.sample_rows(q.shape, 9, seed=2)
+    assert np.allclose(orc.lse_rows_f64(q, k, rows, causal=causal),
+                       [lse[b, h, i] for b, h, i in rows], rtol=0, atol=1e-12)
+    st = orc.block_stats_f64(q, k, 4, causal=causal)
+    assert np.allclose(st["lse_prefix"][-1], lse, rtol=0, atol=1e-12)
+    for n in range(1, st["lse_block"].shape[0]):
+        assert np.allclose(st["lse_prefix"][n], np.logaddexp(st["lse_prefix"][n - 1],
+                                                             st["lse_block"][n]), atol=1e-12)
+    for n in range(st["lse_block"].shape[0]):     # each block: masked scores of its keys
+        blk = s[..., 4 * n:4 * n + 4]
+        assert np.allclose(st["lse_block"][n], torch.logsumexp(blk, dim=-1).numpy(), atol=1e-12)
+        assert np.allclose(st["max_block"][n], blk.amax(dim=-1).numpy())

@@ -17,6 +17,10 @@ summary for the same workload and tile, null when there is none), and
 bounded sample of the same workload (a few query rows of head 0 against all
 keys; the oracle's CPU restatement, a reported baseline only).
 
+``--causal top_left|bottom_right`` times the same workload under a causal
+mask (not the headline metric): FLOPs then count only the (query, key)
+pairs the mask leaves, 4*B*Hq*D*pairs.
+
 ``--copy-mib M`` additionally runs ``--copy-reps`` plain device-to-device
 copies of M MiB after the timed region, untimed: the calibration kernel the
 traffic summary scales the FETCH_SIZE and WRITE_SIZE counters by.
@@ -47,6 +51,8 @@ def parse_args(argv=None):
     p.add_argument("--case", type=int, default=3, help="configuration index c0..c4")
     p.add_argument("--backend", default="hip_fa_fp32acc")
     p.add_argument("--kernel", type=int, default=0, help="tile configuration (0 = automatic)")
+    p.add_argument("--causal", default="none", choices=("none", "top_left", "bottom_right"),
+                   help="attention mask (the headline workload is full attention)")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -137,7 +143,7 @@ def main(argv=None):
 
     from fa_amd.core import registry
     from fa_amd.problem.canonical import build_canonical
-    from fa_amd.problem.cases import CASES
+    from fa_amd.problem.cases import CASES, visible_pairs
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -159,12 +165,15 @@ def main(argv=None):
 
     acc = getattr(spec, "ACC", None)
     tile_name = None
+    if acc is None and args.causal != "none":
+        print(f"--causal needs a HIP backend, not {args.backend}", file=sys.stderr)
+        return 2
     if acc is not None:
         op = Operator(hip_common.project(case, prebuilt=True).artifact_paths()[0],
-                      AttentionConfig(acc=acc, kernel=args.kernel))
+                      AttentionConfig(acc=acc, kernel=args.kernel, causal=args.causal))
         tile_name = op.kernel_name(canonical["q"].shape, canonical["k"].shape)
-        if args.kernel:
-            # Explicit tile configuration (tuning runs).
+        if args.kernel or args.causal != "none":
+            # Explicit tile configuration (tuning runs) or a causal mask.
             call = lambda: op(canonical["q"], canonical["k"], canonical["v"])  # noqa: E731
 
     for _ in range(args.warmup):
@@ -178,7 +187,9 @@ def main(argv=None):
     end.record(stream)
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
-    tflops = case.flops / (ms * 1e-3) / 1e12
+    flops = (4 * case.batch * case.heads_q * case.dim
+             * visible_pairs(case.seq_len, case.seq_len, args.causal))
+    tflops = flops / (ms * 1e-3) / 1e12
 
     if args.copy_mib:
         n = args.copy_mib << 20
@@ -192,6 +203,9 @@ def main(argv=None):
         del src, dst
 
     workload_key = f"{args.backend} c{args.case} {case.name} tile={tile_name}"
+    if args.causal != "none":
+        workload_key += f" causal={args.causal}"
+    mask = "non-causal" if args.causal == "none" else f"causal ({args.causal})"
     line = {
         "metric": "fwd ms & QK/PV TFLOPS (% FP16 MFMA peak), B=2 N=131072 Hq=12 D=128",
         "value": round(tflops, 2),
@@ -206,8 +220,9 @@ def main(argv=None):
         "dtype": "fp16",
         "data": "synthetic",
         "config": {
-            "workload": f"c{args.case} {case.name} non-causal GQA forward, "
+            "workload": f"c{args.case} {case.name} {mask} GQA forward, "
                         f"{acc or 'fp32'}-accumulate",
+            "causal": args.causal,
             "backend": args.backend,
             "tile": tile_name,
             "batch": case.batch, "seq_len": case.seq_len, "heads_q": case.heads_q,

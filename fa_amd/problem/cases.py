@@ -87,3 +87,25 @@ VARIANTS = {
 
 def index_of(case: Case) -> int:
     return CASES.index(case)
+
+
+def visible_pairs(seq_q: int, seq_k: int, causal: str = "none") -> int:
+    """(query, key) pairs one head computes: Nq*Nk for full attention; under a
+    causal mask row i sees min(Nk, i + off + 1) keys (off = 0 top-left,
+    Nk - Nq bottom-right, none when negative). The FLOP count of a masked
+    forward is 4*B*Hq*D times this (masked-out pairs are not counted)."""
+    if causal == "none":
+        return seq_q * seq_k
+    off = {"top_left": 0, "bottom_right": seq_k - seq_q}[causal]
+
+    def upto(n):                      # sum_{i < n} min(Nk, max(0, i + off + 1))
+        total = 0
+        lo = max(0, -off)            # rows before lo see nothing
+        hi = min(n, max(lo, seq_k - off - 1))   # rows lo..hi-1 see i + off + 1 < Nk keys
+        if hi > lo:
+            total += (hi - lo) * (lo + off + 1) + (hi - lo) * (hi - lo - 1) // 2
+        if n > max(lo, hi):
+            total += (n - max(lo, hi)) * seq_k
+        return total
+
+    return upto(seq_q)

@@ -370,3 +370,20 @@ class ProfileNameTests(unittest.TestCase):
 
 if __name__ == "__main__":
     unittest.main()
+
+
+def test_visible_pairs_counts_masked_flops():
+    from fa_amd.problem.cases import visible_pairs
+
+    def brute(nq, nk, causal):
+        if causal == "none":
+            return nq * nk
+        off = 0 if causal == "top_left" else nk - nq
+        return sum(min(nk, max(0, i + off + 1)) for i in range(nq))
+
+    for nq in (1, 2, 5, 300, 1100):
+        for nk in (1, 3, 300, 1100):
+            for causal in ("none", "top_left", "bottom_right"):
+                assert visible_pairs(nq, nk, causal) == brute(nq, nk, causal), (nq, nk, causal)
+    n = 131072
+    assert visible_pairs(n, n, "top_left") == n * (n + 1) // 2

@@ -1,16 +1,25 @@
 """GPU parity of the HIP forward against the CPU oracle, through the C ABI.
 
 Every case prints its name before the GPU work starts. Tolerances (north-star
-bar, checked against the float64 oracle):
-  FP32-accumulate: |out - exact| <= 2e-3 + 2^-10 * |exact|
-  FP16-accumulate: |out - exact| <= 1e-2 + 1e-2 * |exact|
-For FP32 the relative term is one FP16 output ulp: for |exact| >= 4 (stress
-inputs reach |O| ~ 30) a single FP16 ulp of the output already exceeds 2e-3,
-so no FP16 result can meet a purely absolute 2e-3 there; for the N(0,1)
-configs |O| < 0.5 and the term stays below 5e-4. For FP16 the relative term is
-the reference harness's own rtol (core/runner.py:67, assert_close with
-atol = rtol = 1e-2): an FP16 O accumulator holding |O| ~ 16 rounds each merge
-at 2^-7, so a purely absolute 1e-2 is out of reach on stress inputs.
+bar, checked against the float64 oracle, elementwise):
+  FP32-accumulate: |out - exact| <= 2e-3 + 2^-10 |O| + 2^-11 (A + |O|)
+  FP16-accumulate: |out - exact| <= 1e-2 + 1e-2 |O| + 2^-11 (A + |O|)
+where O is the exact output and A = sum_j w_j |v_j| (the softmax-weighted
+mean of |v|, i.e. attention applied to |v|). The terms:
+  * 2^-10 |O| (FP32): one FP16 output ulp -- for |O| >= 4 (stress inputs reach
+    |O| ~ 30) a single ulp already exceeds 2e-3, so no FP16 result can meet a
+    purely absolute 2e-3 there; for the N(0,1) configs |O| < 0.5.
+  * 1e-2 |O| (FP16): the reference harness's own rtol (core/runner.py:67,
+    assert_close with atol = rtol = 1e-2): an FP16 O accumulator holding
+    |O| ~ 16 rounds each merge at 2^-7.
+  * 2^-11 (A + |O|): P is rounded to FP16 for the PV matrix product (as in
+    every reference variant), each weight to within 2^-11 relative; the same
+    rounded weights normalise O, so the output moves by
+    sum_j w_j d_j (v_j - O) with |d_j| <= 2^-11, at most 2^-11 (A + |O|). On
+    peaked rows whose few dominant keys carry the x8 value rows of c4 this
+    reaches ~1e-2; on N(0,1) inputs it is ~4e-4.
+The N(0,1) configurations must also meet the north-star's literal absolute
+bar (2e-3 FP32, 1e-2 FP16) outright.
 """
 
 import numpy as np
@@ -47,9 +56,17 @@ def run(op, t):
     return out.float().cpu().numpy()
 
 
-def check(out, exact, acc, what):
+# Relative rounding of one FP16 probability (round to nearest, normal range).
+P_ROUND = 2.0 ** -11
+
+
+def check(out, exact, acc, what, wabs=None):
+    """Elementwise bound of the module docstring; ``wabs`` = attention applied
+    to |v| (the P-rounding term is left out when it is not given)."""
     err = np.abs(out.astype(np.float64) - exact)
     bound = ATOL[acc] + RTOL[acc] * np.abs(exact)
+    if wabs is not None:
+        bound = bound + P_ROUND * (np.asarray(wabs, dtype=np.float64) + np.abs(exact))
     worst = float(err.max())
     rel = float((err / np.maximum(np.abs(exact), 1e-30)).max())
     excess = float((err - bound).max())
@@ -93,7 +110,10 @@ def test_small_shapes_vs_f64(ops, case, acc):
     say(f"case {case.name} acc={acc}")
     cpu, dev = inputs(case, seed=1)
     exact = orc.attention_f64(cpu["q"], cpu["k"], cpu["v"])
-    check(run(ops[acc], dev), exact, acc, case.name)
+    wabs = orc.attention_f64(cpu["q"], cpu["k"], cpu["v"].abs())
+    worst = check(run(ops[acc], dev), exact, acc, case.name, wabs)
+    if case.dist == "normal":
+        assert worst <= ATOL[acc]
 
 
 @pytest.mark.parametrize("acc", ["fp32", "fp16"])
@@ -215,13 +235,14 @@ def test_ragged_stress_and_repeat(ops):
     v = torch.randn(1, 2, 1537, 128, generator=g).half()
     v[:, :, ::19] *= 8
     exact = orc.attention_f64(q, k, v)
+    wabs = orc.attention_f64(q, k, v.abs())
     dev = [t.cuda() for t in (q, k, v)]
     for acc, op in ops.items():
         first = op(*dev).clone()
         again = op(*dev).clone()          # the padded workspace is rebuilt each call
         torch.cuda.synchronize()
         assert bool(torch.equal(first, again)), acc
-        check(first.float().cpu().numpy(), exact, acc, "ragged stress")
+        check(first.float().cpu().numpy(), exact, acc, "ragged stress", wabs)
 
 
 def test_lse_every_tile_and_plain_fa_fwd_unchanged(library_path):
@@ -325,10 +346,11 @@ def test_every_tile_config(library_path, kernel, shape):
     k = (torch.randn(2, 1, nk, 128, generator=g) * sig).half()
     v = torch.randn(2, 1, nk, 128, generator=g).half()
     exact = orc.attention_f64(q, k, v)
+    wabs = orc.attention_f64(q, k, v.abs())
     dev = {"q": q.cuda(), "k": k.cuda(), "v": v.cuda()}
     for acc in ("fp32", "fp16"):
         op = Operator(library_path, AttentionConfig(acc=acc, kernel=kernel))
-        check(run(op, dev), exact, acc, f"tile{kernel}")
+        check(run(op, dev), exact, acc, f"tile{kernel}", wabs)
 
 
 def kernel_name(kernel):
@@ -353,7 +375,10 @@ def test_full_size_sampled_rows(ops, idx, acc):
     got = out[idx_t[:, 0], idx_t[:, 1], idx_t[:, 2]].float().cpu().numpy()
     assert bool(np.all(np.isfinite(out.float().abs().amax(dim=(2, 3)).cpu().numpy())))
     exact = orc.attention_rows_f64(cpu["q"], cpu["k"], cpu["v"], rows)
-    check(got, exact, acc, f"c{idx} sampled rows")
+    wabs = orc.attention_rows_f64(cpu["q"], cpu["k"], cpu["v"].abs(), rows)
+    worst = check(got, exact, acc, f"c{idx} sampled rows", wabs)
+    if case.dist == "normal":
+        assert worst <= ATOL[acc]
     got_lse = lse[idx_t[:, 0], idx_t[:, 1], idx_t[:, 2]].cpu().numpy()
     check_lse(got_lse, orc.lse_rows_f64(cpu["q"], cpu["k"], rows), f"c{idx} sampled rows")
     del dev, out
@@ -401,7 +426,8 @@ def test_causal_vs_f64(library_path, b, hq, hkv, nq, nk, sig, causal, acc):
     out, lse = op(q.cuda(), k.cuda(), v.cuda(), return_lse=True)
     torch.cuda.synchronize()
     out = out.float().cpu().numpy()
-    check(out, orc.attention_f64(q, k, v, causal=causal), acc, "causal")
+    check(out, orc.attention_f64(q, k, v, causal=causal), acc, "causal",
+          orc.attention_f64(q, k, v.abs(), causal=causal))
     exact_lse = orc.lse_f64(q, k, causal=causal)
     check_lse(lse.cpu().numpy(), exact_lse, "causal")
     empty = np.isneginf(exact_lse)
@@ -459,7 +485,8 @@ def test_causal_capture_statistics(library_path, causal, nq, nk, acc):
     torch.cuda.synchronize()
     m, l, alpha, z = (t.double().cpu().numpy() for t in op.last["stats"])
     ex = orc.block_stats_f64(q, k, op.last["block_keys"], causal=causal)
-    check(out.float().cpu().numpy(), orc.attention_f64(q, k, v, causal=causal), acc, "capture O")
+    check(out.float().cpu().numpy(), orc.attention_f64(q, k, v, causal=causal), acc, "capture O",
+          orc.attention_f64(q, k, v.abs(), causal=causal))
     with np.errstate(divide="ignore", invalid="ignore"):
         total = m + np.log(l)
         assert _close_or_both_neginf(total, ex["lse_prefix"], LSE_ATOL)
@@ -496,9 +523,73 @@ def test_causal_full_size_sampled_rows(library_path, idx, acc, causal):
     got = out[idx_t[:, 0], idx_t[:, 1], idx_t[:, 2]].float().cpu().numpy()
     assert bool(np.all(np.isfinite(out.float().abs().amax(dim=(2, 3)).cpu().numpy())))
     exact = orc.attention_rows_f64(cpu["q"], cpu["k"], cpu["v"], rows, causal=causal)
-    check(got, exact, acc, f"causal c{idx} sampled rows")
+    worst = check(got, exact, acc, f"causal c{idx} sampled rows")
+    assert worst <= ATOL[acc]
     got_lse = lse[idx_t[:, 0], idx_t[:, 1], idx_t[:, 2]].cpu().numpy()
     check_lse(got_lse, orc.lse_rows_f64(cpu["q"], cpu["k"], rows, causal=causal),
               f"causal c{idx} sampled rows")
+    del dev, out
+    torch.cuda.empty_cache()
+
+
+# --------------------------------------------------------------------------- #
+# full-size, every row: against the canonical FP32 formula run on the GPU
+# --------------------------------------------------------------------------- #
+def fp32_formula_check(out, q, k, v, acc, causal="none", chunk_elems=1 << 28):
+    """Compare every row of ``out`` with softmax(q k^T * scale) v computed in
+    FP32 torch on the GPU (the reference's canonical formula,
+    backends/expert_v2/impl.py:701-716, kept in FP32 instead of rounded to
+    FP16), chunked over query rows. Returns (max |diff|, max excess over the
+    variant's bound)."""
+    b_, hq, nq, d = q.shape
+    hkv, nk = k.shape[1], k.shape[2]
+    group = hq // hkv
+    scale = d ** -0.5
+    off = {"none": None, "top_left": 0, "bottom_right": nk - nq}[causal]
+    rows = max(1, chunk_elems // nk)
+    worst, excess = 0.0, -np.inf
+    keys = torch.arange(nk, device=q.device)
+    for b in range(b_):
+        for h in range(hq):
+            kt = k[b, h // group].float().t().contiguous()
+            vf = v[b, h // group].float()
+            for r0 in range(0, nq, rows):
+                r1 = min(nq, r0 + rows)
+                s = torch.matmul(q[b, h, r0:r1].float(), kt).mul_(scale)
+                if off is not None:
+                    lim = torch.arange(r0, r1, device=q.device) + off
+                    s.masked_fill_(keys[None, :] > lim[:, None], float("-inf"))
+                w = torch.softmax(s, dim=-1)
+                del s
+                ref = torch.nan_to_num(torch.matmul(w, vf), nan=0.0)     # rows without keys
+                wabs = torch.nan_to_num(torch.matmul(w, vf.abs()), nan=0.0)
+                del w
+                err = (out[b, h, r0:r1].float() - ref).abs()
+                bound = ATOL[acc] + RTOL[acc] * ref.abs() + P_ROUND * (wabs + ref.abs())
+                worst = max(worst, float(err.max()))
+                excess = max(excess, float((err - bound).max()))
+    return worst, excess
+
+
+FULL_ROWS = [(1, "fp32", "none"), (2, "fp32", "none"), (2, "fp16", "none"), (3, "fp32", "none"),
+             (4, "fp32", "none"), (4, "fp16", "none"), (2, "fp32", "top_left")]
+
+
+@pytest.mark.parametrize("idx,acc,causal", FULL_ROWS,
+                         ids=[f"c{i}-{a}-{c}" for i, a, c in FULL_ROWS])
+def test_full_size_every_row_vs_fp32_formula(library_path, idx, acc, causal):
+    case = CASES[idx]
+    say(f"case every row c{idx} {case.name} acc={acc} causal={causal}: generating inputs")
+    _, dev = inputs(case)
+    say(f"case every row c{idx} {case.name} acc={acc} causal={causal}: launching")
+    op = Operator(library_path, AttentionConfig(acc=acc, causal=causal))
+    out = op(dev["q"], dev["k"], dev["v"])
+    torch.cuda.synchronize()
+    say(f"case every row c{idx}: comparing with the FP32 formula on the GPU")
+    worst, excess = fp32_formula_check(out, dev["q"], dev["k"], dev["v"], acc, causal)
+    say(f"  c{idx} every row acc={acc} causal={causal} max_abs={worst:.3e} max_excess={excess:.3e}")
+    assert excess <= 0, f"max abs error {worst:.3e} exceeds the bound by {excess:.3e}"
+    if case.dist == "normal":
+        assert worst <= ATOL[acc], f"max abs error {worst:.3e} above the north-star bar"
     del dev, out
     torch.cuda.empty_cache()

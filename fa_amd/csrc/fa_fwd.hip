@@ -41,6 +41,8 @@
 #include <stdint.h>
 #include <math.h>
 
+#include <type_traits>
+
 #include "../../include/fa_hip.h"
 
 namespace {
@@ -54,6 +56,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int HD = 128;               // head dimension
 constexpr int VT_GROUP = 64;          // keys per prep-kernel workgroup
 constexpr float NEG_BIG = -1.0e30f;   // finite "minus infinity" for the running max
+// Added to the score of a masked key: far below any real score
+// (|scale * q.k| <= 128 * 65504^2 ~ 5.5e11) and below NEG_BIG, so the key
+// gets P = 0 and can neither raise the running max nor start it.
+constexpr float MASKED = -1.0e38f;
 constexpr double LOG2E = 1.4426950408889634;
 constexpr float LN2 = 0.6931471805599453f;
 
@@ -504,8 +510,8 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   const size_t grow = (size_t)bh * seq_q + (row_ok ? row : seq_q - 1);
 
   // Last key this lane's row sees (klim) and the smallest such limit over the
-  // wave (klim_w, wave-uniform: the wave's first row); blocks past klim_w need
-  // per-element masking. With the causal mask the workgroup streams only the
+  // wave (klim_w, wave-uniform: the wave's first row); blocks reaching past
+  // klim_w take the key loop's masked part. With the causal mask the workgroup streams only the
   // key blocks its last row sees.
   int nblk = seq_k / BN;
   int klim = nk_valid - 1, klim_w = nk_valid - 1;
@@ -696,7 +702,7 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
 
   // VALU step: online softmax of S(j) into P(j) (and, for the FP16
   // accumulator, the merge of the PV(j-1) partial computed by MFMA step j).
-  auto valu_step = [&](int key0) {
+  auto valu_step = [&](int key0, auto masked) {
     if constexpr (ACC16) {
       const _Float16 a16 = (_Float16)alpha_prev;
       const h2 a2 = {a16, a16};
@@ -709,15 +715,21 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
         }
     }
     // Keys past the row's limit (zero padding of a ragged last block, keys
-    // beyond the causal diagonal) score -inf: they get P = 0. S^T register r
-    // of lane half hf holds key 32t + 8(r / 4) + 4hf + r % 4 of the block.
-    if (key0 + BN - 1 > klim_w) {
+    // beyond the causal diagonal) get MASKED added to their score, so P = 0.
+    // S^T register r of lane half hf holds key 32t + 8(r / 4) + 4hf + r % 4
+    // of the block. The penalty weight clamp(key - limit, 0, 1) is computed
+    // in float arithmetic: a per-element compare and select would hold up to
+    // 64 lane masks in scalar registers, and that pressure spills scalar
+    // registers across the whole key loop.
+    if constexpr (decltype(masked)::value) {
       const int lim = klim - key0 - 4 * hf;
 #pragma unroll
       for (int t = 0; t < KT; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (32 * t + 8 * (r >> 2) + (r & 3) > lim) s[t][r] = -INFINITY;
+        for (int r = 0; r < 16; ++r) {
+          const float d = (float)(32 * t + 8 * (r >> 2) + (r & 3) - lim);
+          s[t][r] = __builtin_fmaf(__builtin_amdgcn_fmed3f(d, 0.f, 1.f), MASKED, s[t][r]);
+        }
     }
     // Row max as a balanced 3-ary tree of v_maximum3 (independent maxima
     // issue back to back; a running max would be one long dependent chain).
@@ -796,30 +808,44 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   // j % NS, the ring slot of K(j); V(j-1) sits in slot (j - 1) % NS. Pair j
   // loads K(j+NS-1) into slot (j-1) % NS and V(j+NS-2) into slot (j-2) % NS,
   // the slots pair j-1 finished with.
+  // Each wave runs its key loop in two parts: blocks j < nfull, which every
+  // row of the wave sees whole, with no mask code at all, then the rest
+  // (the ragged tail, the causal diagonal), which always applies the
+  // per-element mask. A wave-uniform test inside one loop measured 1-3%
+  // slower than no test, even when never taken.
+  const std::integral_constant<bool, false> unmasked;
+  const std::integral_constant<bool, true> masked;
+  const int nfull = klim_w + 1 < BN ? 0 : min(nblk, (klim_w + 1) / BN);
   int sl = 0;
   if (grp == 0) {
-    for (int j = 0; j < nblk; ++j) {
+    auto pair = [&](int j, auto mask) {
       const int sp = prev(sl);
       mfma_step(kslot(sl), vslot(sp), true, min(j + NS - 1, last), sp, min(j + NS - 2, last),
                 prev(sp));             // phase 2j: pair j starts
       lds_barrier();
-      valu_step(j * BN);             // phase 2j + 1
+      valu_step(j * BN, mask);       // phase 2j + 1
       wait_dma(keep);                // K(j+1), V(j) have landed
       lds_barrier();
       sl = next(sl);
-    }
+    };
+    int j = 0;
+    for (; j < nfull; ++j) pair(j, unmasked);
+    for (; j < nblk; ++j) pair(j, masked);
     mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0);   // phase 2 nblk: PV(nblk - 1)
     lds_barrier();
     lds_barrier();                           // phase 2 nblk + 1: idle
   } else {
     lds_barrier();                   // phase 0: this group idles
-    for (int j = 0; j < nblk; ++j) {
+    auto pair = [&](int j, auto mask) {
       mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0);   // phase 2j + 1
       lds_barrier();
-      valu_step(j * BN);             // phase 2j + 2
+      valu_step(j * BN, mask);       // phase 2j + 2
       lds_barrier();
       sl = next(sl);
-    }
+    };
+    int j = 0;
+    for (; j < nfull; ++j) pair(j, unmasked);
+    for (; j < nblk; ++j) pair(j, masked);
     mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0);   // phase 2 nblk + 1: PV(nblk - 1)
     lds_barrier();
   }

@@ -556,7 +556,6 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   // source offset inside a block is fixed, so it is computed once.
   const int dw = SPLIT_HI ? (wave_u & 3) : (wave_u >> 1);
   int dma_off[NIW];
-  const int n_dma = grp == 0 ? (NI - dw + 3) / 4 : 0;   // instructions this wave issues per pair
 #pragma unroll
   for (int m = 0; m < NIW; ++m) {
     const int q = dw + 4 * m;
@@ -801,7 +800,13 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   auto prev = [](int sl) { return sl == 0 ? NS - 1 : sl - 1; };
   auto kslot = [&](int sl) { return kbase + sl * KBYTES; };
   auto vslot = [&](int sl) { return vbase + sl * VBYTES; };
-  const int keep = (NS - 2) * n_dma;     // loads of later pairs still in flight
+  // Loads of later pairs a group-0 wave may leave in flight at its wait:
+  // (NS - 2) pairs' worth, counted for the waves that issue one instruction
+  // fewer when NI is not a multiple of 4. The others then also wait for
+  // their oldest load of pair j+1, issued a phase pair earlier. A constant
+  // count makes the wait one s_waitcnt (a per-wave count cost a branch
+  // chain in every iteration).
+  constexpr int keep = (NS - 2) * (NI % 4 != 0 ? NIW - 1 : NIW);
 
   // Phase 2j + grp is this wave's MFMA step for block j, phase 2j + grp + 1
   // its VALU step; both groups pass the same 2 * nblk + 2 barriers. sl is

@@ -567,8 +567,19 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
       dma_off[m] = d * seq_k * 2 + (ch < VCPR ? ch : 0) * 16;
     }
   }
-  const char* kbytes = reinterpret_cast<const char*>(kp);
-  const char* vbytes = reinterpret_cast<const char*>(vp);
+  // The loads are buffer loads through one descriptor per operand (base =
+  // this KV head's K or V^T, range = its seq_k * 256 bytes, so the hardware
+  // bounds-checks every lane): the per-lane offset is dma_off, the block
+  // offset a wave-uniform scalar. Buffer (MUBUF) loads rather than
+  // global_load_lds: the compiler counts a FLAT-encoded load into LDS as a
+  // possible LDS access of unknown order and waits for every outstanding LDS
+  // read (lgkmcnt(0)) after each one, which drained the operand prefetch
+  // of the MFMA step; buffer loads are counted on vmcnt only.
+  constexpr int RSRC_WORD3 = 0x00020000;   // gfx9 raw-buffer descriptor: 32-bit data format
+  const __amdgpu_buffer_rsrc_t krsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kp, (short)0, seq_k * (HD * 2), RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t vrsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vp, (short)0, seq_k * (HD * 2), RSRC_WORD3);
   // DMA instruction m of this wave for K block kb -> ring slot ks and V^T
   // block vb -> slot vs. Branch free: the K/V^T choice is a select on
   // wave-uniform values; only a wave's last instruction can be absent.
@@ -576,10 +587,11 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
     const int q = dw + 4 * m;
     if (m == NIW - 1 && NI % 4 != 0 && q >= NI) return;
     const bool isk = q < KI;
-    const char* src = (isk ? kbytes + (size_t)kb * (BN * HD * 2) : vbytes + (size_t)vb * (BN * 2)) +
-                      dma_off[m];
     char* dst = isk ? kbase + ks * KBYTES + q * 1024 : vbase + vs * VBYTES + (q - KI) * 1024;
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(isk ? krsrc : vrsrc,
+                                             (__attribute__((address_space(3))) void*)dst, 16,
+                                             dma_off[m], isk ? kb * (BN * HD * 2) : vb * (BN * 2),
+                                             0, 0);
   };
   auto issue = [&](int kb, int ks, int vb, int vs) {
 #pragma unroll

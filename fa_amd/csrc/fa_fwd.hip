@@ -990,12 +990,12 @@ const TileConfig kTiles[] = {
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 // Automatic choice (fa_problem.kernel == 0): the first of these 1-based tile
-// indices, fastest first (measured at N = 32768), that fits the problem (masks
-// tails, or its query-row and key granularity divide Nq and Nk). The FP16
-// accumulator's 128-key tile spills registers, so that variant prefers the
-// 64-key ring.
+// indices, fastest first (measured at N = 32768 and 65536), that fits the
+// problem (masks tails, or its query-row and key granularity divide Nq and
+// Nk). The FP16 accumulator's 128-key tile spills registers, so that variant
+// prefers a 64-key ring.
 constexpr int kAutoOrderFp32[] = {5, 4, 3, 2, 1};
-constexpr int kAutoOrderFp16[] = {4, 3, 5, 2, 1};
+constexpr int kAutoOrderFp16[] = {3, 4, 5, 2, 1};
 static_assert(sizeof(kAutoOrderFp32) == sizeof(int) * kNumTiles &&
                   sizeof(kAutoOrderFp16) == sizeof(int) * kNumTiles,
               "every tile appears in each automatic order");

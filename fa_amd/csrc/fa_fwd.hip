@@ -424,8 +424,8 @@ __device__ __forceinline__ void lds_barrier() {
 //
 // LDS holds a ring of NS K blocks and NS V^T blocks (NS >= 2). Phase pair t
 // (phases 2t, 2t+1) reads K(t) and V(t-1). During its MFMA step of pair t,
-// group 0 issues the direct-to-LDS loads (global_load_lds_dwordx4, 1 KiB per
-// wave instruction) of K(t+NS-1) and V(t+NS-2) into the ring slots pair t-1
+// group 0 issues the direct-to-LDS loads (buffer_load_dwordx4 ... lds, 1 KiB
+// per wave instruction) of K(t+NS-1) and V(t+NS-2) into the ring slots pair t-1
 // finished with, one load every few MFMAs so the vector-memory issue never
 // stalls the wave for long; the VALU steps carry no load work. Group 0 waits
 // for its pair t+2-NS loads at the end of pair t, before the barrier that

@@ -41,3 +41,31 @@ def test_runner_check_mode_subprocess():
     print(r.stdout[-500:], flush=True)
     assert r.returncode == 0
     assert "CHECK B1_S4096_Q12_KV1_D128 backend=hip_fa_fp32acc PASS" in r.stdout
+
+
+@pytest.mark.parametrize("causal", ["none", "top_left"])
+def test_bench_json_line(causal):
+    """bench.py's one JSON line at c0: the fields the driver reads, the roofline
+    consistent with the value, and the CPU baseline of the oracle port."""
+    import json
+    import os
+    import subprocess
+    import sys
+
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print(f"case bench.py c0 causal={causal}", flush=True)
+    proc = subprocess.run([sys.executable, os.path.join(repo, "bench.py"), "--case", "0",
+                           "--steps", "3", "--warmup", "1", "--cpu-seconds", "1",
+                           "--causal", causal], capture_output=True, text=True, timeout=240)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    line = json.loads(proc.stdout.strip().splitlines()[-1])
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+                "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config",
+                "roofline", "cpu_baseline"):
+        assert key in line, key
+    assert line["n_gpus"] == 1 and line["steps"] == 3 and line["value"] > 0
+    assert line["config"]["causal"] == causal and line["config"]["tile"].startswith("pp_")
+    roof = line["roofline"]
+    assert roof["bound"] == "mfma" and abs(roof["frac"] - line["value"] / roof["peak"]) < 1e-3
+    cpu = line["cpu_baseline"]
+    assert cpu["kind"] == "port" and cpu["value"] > 0 and cpu["cores"] >= 1

@@ -90,3 +90,13 @@ def test_counter_summary(tmp_path):
     s = counters.summarize(str(tmp_path / "c"), "hip_fa_", ["SQ_BUSY_CYCLES"])
     val, n, kernel = s["SQ_BUSY_CYCLES"]
     assert (n, kernel) == (2, "hip_fa_fp32acc_kernel") and val == 11.0   # median of 12, 10
+
+
+def test_bench_cli_contract():
+    import bench
+
+    args = bench.parse_args([])
+    assert (args.gpus, args.case, args.causal, args.kernel) == (1, 3, "none", 0)
+    assert bench.parse_args(["--causal", "bottom_right"]).causal == "bottom_right"
+    # More than one GPU is refused before anything touches a device.
+    assert bench.main(["--gpus", "2"]) == 2

@@ -593,3 +593,20 @@ def test_full_size_every_row_vs_fp32_formula(library_path, idx, acc, causal):
         assert worst <= ATOL[acc], f"max abs error {worst:.3e} above the north-star bar"
     del dev, out
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("b,hq,hkv,nq,nk", _random_shapes(6, seed=77))
+def test_random_shapes_causal(library_path, b, hq, hkv, nq, nk):
+    """Seeded random geometry under both causal alignments and both variants."""
+    say(f"case random causal B{b} Hq{hq} Hkv{hkv} nq={nq} nk={nk}")
+    q, k, v = causal_inputs(b, hq, hkv, nq, nk, 1.0, seed=b * 7919 + nq * 31 + nk)
+    dev = [t.cuda() for t in (q, k, v)]
+    for causal in ("top_left", "bottom_right"):
+        exact = orc.attention_f64(q, k, v, causal=causal)
+        exact_lse = orc.lse_f64(q, k, causal=causal)
+        for acc in ("fp32", "fp16"):
+            op = Operator(library_path, AttentionConfig(acc=acc, causal=causal))
+            out, lse = op(*dev, return_lse=True)
+            torch.cuda.synchronize()
+            check(out.float().cpu().numpy(), exact, acc, f"random {causal}")
+            check_lse(lse.cpu().numpy(), exact_lse, f"random {causal} {acc}")

@@ -610,3 +610,21 @@ def test_random_shapes_causal(library_path, b, hq, hkv, nq, nk):
             torch.cuda.synchronize()
             check(out.float().cpu().numpy(), exact, acc, f"random {causal}")
             check_lse(lse.cpu().numpy(), exact_lse, f"random {causal} {acc}")
+
+
+@pytest.mark.parametrize("scale", [1.0, 0.25, 1e-3])
+@pytest.mark.parametrize("causal", ["none", "top_left"])
+def test_custom_scale(library_path, scale, causal):
+    """A softmax scale other than D^-0.5: peaked (1.0), moderate, nearly flat."""
+    say(f"case scale={scale} causal={causal} nq=300 nk=777")
+    q, k, v = causal_inputs(1, 4, 2, 300, 777, 1.0, seed=int(scale * 1000) + len(causal))
+    dev = [t.cuda() for t in (q, k, v)]
+    exact = orc.attention_f64(q, k, v, scale=scale, causal=causal)
+    wabs = orc.attention_f64(q, k, v.abs(), scale=scale, causal=causal)
+    exact_lse = orc.lse_f64(q, k, scale=scale, causal=causal)
+    for acc in ("fp32", "fp16"):
+        op = Operator(library_path, AttentionConfig(acc=acc, causal=causal))
+        out, lse = op(*dev, scale=scale, return_lse=True)
+        torch.cuda.synchronize()
+        check(out.float().cpu().numpy(), exact, acc, f"scale {scale}", wabs)
+        check_lse(lse.cpu().numpy(), exact_lse, f"scale {scale} {acc}")

@@ -8,7 +8,10 @@ Mirrors the reference's operator binding
     ``fa_fwd`` (or ``fa_fwd_lse`` when the per-row log-sum-exp is asked for)
     enqueues the forward on the current torch stream;
   * geometry, dtype, device and layout errors raise ``ValueError`` before any
-    launch; a nonzero library status raises ``RuntimeError("fa_fwd <where>:
+    launch (any [B,H,N,128] view whose last dimension is contiguous and whose
+    rows are 16-byte aligned is accepted: non-contiguous views, such as the
+    sequence-major tensors of FlashAttention-style code, go through
+    ``fa_fwd_strided`` without a copy); a nonzero library status raises ``RuntimeError("fa_fwd <where>:
     <status> (<message>)")``;
   * output and workspace tensors are allocated by torch, cached per
     (shapes, device, config), and the same cached output tensor is returned
@@ -45,6 +48,12 @@ class FaProblem(C.Structure):
     ]
 
 
+class FaStrides(C.Structure):
+    """Element strides of dims B, H, N of q, k, v and o (``fa_strides``)."""
+    _fields_ = [("q", C.c_int64 * 3), ("k", C.c_int64 * 3), ("v", C.c_int64 * 3),
+                ("o", C.c_int64 * 3)]
+
+
 # Every symbol include/fa_hip.h declares, with its ctypes signature.
 SIGNATURES = {
     "fa_fwd_workspace_bytes": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_uint64)]),
@@ -52,6 +61,9 @@ SIGNATURES = {
                          C.c_void_p, C.c_uint64, C.c_void_p]),
     "fa_fwd_lse": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                              C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
+    "fa_fwd_strided": (C.c_int, [C.POINTER(FaProblem), C.POINTER(FaStrides), C.c_void_p,
+                                 C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                 C.c_uint64, C.c_void_p]),
     "fa_fwd_capture_count": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_uint64),
                                        C.POINTER(C.c_int32)]),
     "fa_fwd_capture": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p,
@@ -156,9 +168,13 @@ class Operator:
         if self.config.causal != "none" and (rows, keys) != (1, 1):
             raise ValueError("a causal mask needs a masking tile (kernel 0 or a ping-pong tile)")
         for t in (q, k, v):
-            if t.device.type != "cuda" or t.device != q.device or t.dtype != torch.float16 \
-                    or not t.is_contiguous():
-                raise ValueError("Q/K/V must be contiguous FP16 on the same GPU")
+            if t.device.type != "cuda" or t.device != q.device or t.dtype != torch.float16:
+                raise ValueError("Q/K/V must be FP16 on the same GPU")
+            st = t.stride()
+            if st[3] != 1 or any(x % 8 or x < 0 for x in st[:3]) or st[2] < 128 \
+                    or t.data_ptr() % 16:
+                raise ValueError("Q/K/V must be [B,H,N,128] views with a contiguous last "
+                                 "dimension and 16-byte aligned rows")
 
     def buffers_for(self, q, k, lse=False):
         import torch
@@ -212,6 +228,9 @@ class Operator:
         capture = self.config.capture
         lse = self.buffers_for(q, k, lse=True) if (return_lse or capture) else None
         stats, block = self.stats_for(q, k, prob) if capture else (None, 0)
+        strided = not all(t.is_contiguous() for t in (q, k, v))
+        if strided and capture:
+            raise ValueError("capture mode needs contiguous Q/K/V")
         with torch.cuda.device(q.device):
             need = max(size.value, 16)
             if self.workspace is None or self.workspace.device != q.device \
@@ -221,7 +240,14 @@ class Operator:
             common = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
             tail = (self.workspace.data_ptr(), self.workspace.numel(),
                     C.c_void_p(stream.cuda_stream))
-            if capture:
+            if strided:
+                st = FaStrides()
+                for name, t in (("q", q), ("k", k), ("v", v), ("o", out)):
+                    getattr(st, name)[:] = t.stride()[:3]
+                status = self.lib.fa_fwd_strided(C.byref(prob), C.byref(st), *common,
+                                                 lse.data_ptr() if lse is not None else None,
+                                                 *tail)
+            elif capture:
                 status = self.lib.fa_fwd_capture(C.byref(prob), *common, lse.data_ptr(),
                                                  stats.data_ptr(), stats.numel(), *tail)
             elif return_lse:

@@ -74,7 +74,12 @@ constexpr float LN2 = 0.6931471805599453f;
 // the block's own row sum z relative to m. c is the softmax scale times
 // log2(e). With causal set, query row i sees keys j <= i + causal_off only
 // (causal_off = 0 aligns the mask top-left, Nk - Nq bottom-right); a row that
-// sees no key gets O = 0 and lse = -inf.
+// sees no key gets O = 0 and lse = -inf. qs, ks and os are the element
+// strides of q, of the K buffer read (the caller's k, or its padded
+// contiguous copy) and of o.
+struct Strides {
+  int64_t b, h, n;   // batch, head and row strides in elements; the 128 dims are contiguous
+};
 struct FaArgs {
   const _Float16* q;
   const _Float16* k;
@@ -85,7 +90,14 @@ struct FaArgs {
   int heads_q, group, seq_q, seq_k, nk_valid;
   int causal, causal_off;
   float c;
+  Strides qs, ks, os;
 };
+
+// Row n of head h of batch b of a strided [B, H, N, 128] tensor.
+template <typename T>
+__device__ __forceinline__ T* row_at(T* base, const Strides& st, int b, int h, int n) {
+  return base + (int64_t)b * st.b + (int64_t)h * st.h + (int64_t)n * st.n;
+}
 
 // 16-byte chunk swizzle for an LDS tile whose rows are CPR chunks long.
 // Rows are read 32 at a time at one logical chunk column; the XOR spreads any
@@ -125,18 +137,19 @@ __device__ __forceinline__ int vt_key_of_slot(int slot) {
 // workgroup; keys at or past nk_valid become zeros. With kpad non-null the
 // group's K rows are also copied to kpad[kv][key0 + r] (zero rows past
 // nk_valid), the padded K a masked key tail reads. Grid (nk_pad / 64, B * Hkv),
-// 256 threads; v and k hold nk_valid keys per head, vt and kpad nk_pad.
+// 256 threads; v and k hold nk_valid keys per head with strides vs and ks,
+// vt and kpad are contiguous with nk_pad keys per head.
 __global__ void __launch_bounds__(256) fa_prep_kernel(const _Float16* __restrict__ k,
                                                       const _Float16* __restrict__ v,
                                                       _Float16* __restrict__ vt,
                                                       _Float16* __restrict__ kpad, int nk_valid,
-                                                      int nk_pad) {
+                                                      int nk_pad, int heads_kv, Strides ks,
+                                                      Strides vs) {
   __shared__ _Float16 tile[VT_GROUP][HD + 8];
   const int tid = threadIdx.x;
   const size_t kv = blockIdx.y;
+  const int b = (int)(kv / heads_kv), hk = (int)(kv % heads_kv);
   const int key0 = blockIdx.x * VT_GROUP;
-  const _Float16* src = v + (kv * nk_valid + key0) * HD;
-  const _Float16* ksrc = k + (kv * nk_valid + key0) * HD;
   _Float16* kdst = kpad ? kpad + (kv * nk_pad + key0) * HD : nullptr;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -145,10 +158,10 @@ __global__ void __launch_bounds__(256) fa_prep_kernel(const _Float16* __restrict
     const bool valid = key0 + r < nk_valid;
     const u32x4 zero = {0u, 0u, 0u, 0u};
     *reinterpret_cast<u32x4*>(&tile[r][ch * 8]) =
-        valid ? *reinterpret_cast<const u32x4*>(src + (size_t)r * HD + ch * 8) : zero;
+        valid ? *reinterpret_cast<const u32x4*>(row_at(v, vs, b, hk, key0 + r) + ch * 8) : zero;
     if (kdst)
       *reinterpret_cast<u32x4*>(kdst + (size_t)r * HD + ch * 8) =
-          valid ? *reinterpret_cast<const u32x4*>(ksrc + (size_t)r * HD + ch * 8) : zero;
+          valid ? *reinterpret_cast<const u32x4*>(row_at(k, ks, b, hk, key0 + r) + ch * 8) : zero;
   }
   __syncthreads();
   _Float16* dst = vt + kv * HD * (size_t)nk_pad + key0;
@@ -201,11 +214,10 @@ __device__ __forceinline__ void fa_fwd_body(const FaArgs& args) {
   const int b = bh / heads_q, h = bh - b * heads_q;
   const int heads_kv = heads_q / group;
   const size_t kv = (size_t)b * heads_kv + h / group;
-  const _Float16* kp = k + kv * (size_t)seq_k * HD;
+  const _Float16* kp = row_at(k, args.ks, b, h / group, 0);
   const _Float16* vp = vt + kv * (size_t)HD * seq_k;
-  const size_t row0 = (size_t)bh * seq_q + (size_t)qt * BM + (size_t)wave * (SUB * 32);
-  const _Float16* qp = q + row0 * HD;
-  _Float16* op = o + row0 * HD;
+  const int rw0 = qt * BM + wave * (SUB * 32);   // this wave's first query row in (b, h)
+  const size_t row0 = (size_t)bh * seq_q + rw0;   // its index in [B * Hq * Nq] (lse)
 
   // Q^T operand fragments: lane holds query row l32, dims 16kk+8hf..+7.
   h8 qf[SUB][8];
@@ -213,7 +225,8 @@ __device__ __forceinline__ void fa_fwd_body(const FaArgs& args) {
   for (int u = 0; u < SUB; ++u)
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
-      qf[u][kk] = *reinterpret_cast<const h8*>(qp + (size_t)(u * 32 + l32) * HD + kk * 16 + hf * 8);
+      qf[u][kk] = *reinterpret_cast<const h8*>(row_at(q, args.qs, b, h, rw0 + u * 32 + l32) +
+                                               kk * 16 + hf * 8);
 
   u32x4 kreg[KLD], vreg[VLD];
   auto gload = [&](int blk) {
@@ -222,7 +235,7 @@ __device__ __forceinline__ void fa_fwd_body(const FaArgs& args) {
     for (int j = 0; j < KLD; ++j) {
       const int i = tid + j * NT;
       const int r = i >> 4, ch = i & 15;
-      kreg[j] = *reinterpret_cast<const u32x4*>(kp + (size_t)(key0 + r) * HD + ch * 8);
+      kreg[j] = *reinterpret_cast<const u32x4*>(kp + (int64_t)(key0 + r) * args.ks.n + ch * 8);
     }
 #pragma unroll
     for (int j = 0; j < VLD; ++j) {
@@ -384,7 +397,7 @@ __device__ __forceinline__ void fa_fwd_body(const FaArgs& args) {
     const float inv = 1.f / l;
     if (args.lse && hf == 0)
       args.lse[row0 + u * 32 + l32] = (__builtin_amdgcn_logf(l) + m[u] * c) * LN2;
-    _Float16* orow = op + (size_t)(u * 32 + l32) * HD;
+    _Float16* orow = row_at(o, args.os, b, h, rw0 + u * 32 + l32);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
@@ -503,11 +516,13 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   const int b = bh / heads_q, h = bh - b * heads_q;
   const int heads_kv = heads_q / group;
   const size_t kv = (size_t)b * heads_kv + h / group;
-  const _Float16* kp = k + kv * (size_t)seq_k * HD;
+  const _Float16* kp = row_at(k, args.ks, b, h / group, 0);
   const _Float16* vp = vt + kv * (size_t)HD * seq_k;
   const int row = qt * BM + wave_u * 32 + l32;          // this lane's query row in (b, h)
   const bool row_ok = row < seq_q;
-  const size_t grow = (size_t)bh * seq_q + (row_ok ? row : seq_q - 1);
+  const int rowc = row_ok ? row : seq_q - 1;            // the row it loads
+  const size_t grow = (size_t)bh * seq_q + rowc;        // its index in [B * Hq * Nq] (lse, stats)
+  const int krow = (int)(args.ks.n * 2);                 // K row pitch in bytes
 
   // Last key this lane's row sees (klim) and the smallest such limit over the
   // wave (klim_w, wave-uniform: the wave's first row); blocks reaching past
@@ -542,14 +557,14 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<h4*>(o + grow * HD + dt * 32 + 8 * g + 4 * hf) = zero;
+        *reinterpret_cast<h4*>(row_at(o, args.os, b, h, rowc) + dt * 32 + 8 * g + 4 * hf) = zero;
     return;
   }
 
   h8 qf[8];
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk)
-    qf[kk] = *reinterpret_cast<const h8*>(q + grow * HD + kk * 16 + hf * 8);
+    qf[kk] = *reinterpret_cast<const h8*>(row_at(q, args.qs, b, h, rowc) + kk * 16 + hf * 8);
 
   // Group-0 wave dw issues DMA instructions q = dw + 4m (m < NIW, q < NI);
   // q < KI is K instruction q, otherwise V^T instruction q - KI. The per-lane
@@ -561,23 +576,23 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
     const int q = dw + 4 * m;
     if (q < KI) {
       const int i = q * 64 + lane, r = i / 17, ch = i % 17;
-      dma_off[m] = r * (HD * 2) + (ch < 16 ? ch : 0) * 16;
+      dma_off[m] = r * krow + (ch < 16 ? ch : 0) * 16;
     } else {
       const int i = (q - KI) * 64 + lane, d = i / (VCPR + 1), ch = i % (VCPR + 1);
       dma_off[m] = d * seq_k * 2 + (ch < VCPR ? ch : 0) * 16;
     }
   }
   // The loads are buffer loads through one descriptor per operand (base =
-  // this KV head's K or V^T, range = its seq_k * 256 bytes, so the hardware
-  // bounds-checks every lane): the per-lane offset is dma_off, the block
-  // offset a wave-uniform scalar. Buffer (MUBUF) loads rather than
+  // this KV head's K or V^T, range = the bytes its seq_k rows span, so the
+  // hardware bounds-checks every lane): the per-lane offset is dma_off, the
+  // block offset a wave-uniform scalar. Buffer (MUBUF) loads rather than
   // global_load_lds: the compiler counts a FLAT-encoded load into LDS as a
   // possible LDS access of unknown order and waits for every outstanding LDS
   // read (lgkmcnt(0)) after each one, which drained the operand prefetch
   // of the MFMA step; buffer loads are counted on vmcnt only.
   constexpr int RSRC_WORD3 = 0x00020000;   // gfx9 raw-buffer descriptor: 32-bit data format
   const __amdgpu_buffer_rsrc_t krsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)kp, (short)0, seq_k * (HD * 2), RSRC_WORD3);
+      __builtin_amdgcn_make_buffer_rsrc((void*)kp, (short)0, (seq_k - 1) * krow + HD * 2, RSRC_WORD3);
   const __amdgpu_buffer_rsrc_t vrsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)vp, (short)0, seq_k * (HD * 2), RSRC_WORD3);
   // DMA instruction m of this wave for K block kb -> ring slot ks and V^T
@@ -590,7 +605,7 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
     char* dst = isk ? kbase + ks * KBYTES + q * 1024 : vbase + vs * VBYTES + (q - KI) * 1024;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(isk ? krsrc : vrsrc,
                                              (__attribute__((address_space(3))) void*)dst, 16,
-                                             dma_off[m], isk ? kb * (BN * HD * 2) : vb * (BN * 2),
+                                             dma_off[m], isk ? kb * (BN * krow) : vb * (BN * 2),
                                              0, 0);
   };
   auto issue = [&](int kb, int ks, int vb, int vs) {
@@ -903,7 +918,7 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   const float inv = l > 0.f ? 1.f / l : 0.f;
   if (!row_ok) return;
   if (args.lse && hf == 0) args.lse[grow] = (__builtin_amdgcn_logf(l) + m * c) * LN2;
-  _Float16* orow = o + grow * HD;
+  _Float16* orow = row_at(o, args.os, b, h, rowc);
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
@@ -1076,14 +1091,44 @@ uint64_t capture_count(const fa_problem* p, const TileConfig* tile, const KeyLay
   return 4ull * (uint64_t)(lay.nk_pad / tile->keys) * (uint64_t)(p->batch * p->heads_q * p->seq_q);
 }
 
-int launch(const fa_problem* p, const void* q, const void* k, const void* v, void* o, float* lse,
-           float* stats, uint64_t stats_count, void* workspace, uint64_t workspace_bytes,
-           void* stream) {
+// Strides of a contiguous [B, H, N, 128] tensor.
+Strides contiguous(int64_t heads, int64_t seq) { return Strides{heads * seq * HD, seq * HD, HD}; }
+
+Strides strides_of(const int64_t* s) { return Strides{s[0], s[1], s[2]}; }
+
+// Caller strides must keep every 128-element row 16-byte aligned and rows
+// apart (n >= 128); the K rows of one head must span less than 2^31 bytes
+// (32-bit buffer offsets) unless a padded copy of K is read instead.
+int check_strides(const fa_problem* p, const fa_strides* s, const KeyLayout& lay) {
+  for (const int64_t* t : {s->q, s->k, s->v, s->o})
+    for (int i = 0; i < 3; ++i) {
+      if (t[i] < 0 || t[i] >= ((int64_t)1 << 40)) return FA_ERR_GEOMETRY;
+      if (t[i] % 8) return FA_ERR_ALIGN;
+    }
+  for (const int64_t* t : {s->q, s->k, s->v, s->o})
+    if (t[2] < HD) return FA_ERR_GEOMETRY;
+  if (!lay.pad_k && (p->seq_k - 1) * s->k[2] * 2 + HD * 2 >= ((int64_t)1 << 31)) return FA_ERR_GEOMETRY;
+  return FA_OK;
+}
+
+int launch(const fa_problem* p, const fa_strides* strides, const void* q, const void* k,
+           const void* v, void* o, float* lse, float* stats, uint64_t stats_count,
+           void* workspace, uint64_t workspace_bytes, void* stream) {
   const TileConfig* tile = nullptr;
   int rc = validate(p, &tile);
   if (rc) return rc;
   if (!q || !k || !v || !o) return FA_ERR_NULL;
   const KeyLayout lay = key_layout(p, tile);
+  Strides qs = contiguous(p->heads_q, p->seq_q), os = qs;
+  Strides ks = contiguous(p->heads_kv, p->seq_k), vs = ks;
+  if (strides) {
+    rc = check_strides(p, strides, lay);
+    if (rc) return rc;
+    qs = strides_of(strides->q);
+    ks = strides_of(strides->k);
+    vs = strides_of(strides->v);
+    os = strides_of(strides->o);
+  }
   if (!workspace || workspace_bytes < lay.vt_bytes + lay.k_bytes) return FA_ERR_WORKSPACE;
   for (const void* ptr : {q, k, v, (const void*)o, (const void*)workspace, (const void*)lse,
                           (const void*)stats})
@@ -1098,7 +1143,8 @@ int launch(const fa_problem* p, const void* q, const void* k, const void* v, voi
   (void)hipGetLastError();  // clear any stale error so the checks below see only ours
   dim3 prep_grid((unsigned)(lay.nk_pad / VT_GROUP), (unsigned)(p->batch * p->heads_kv));
   hipLaunchKernelGGL(fa_prep_kernel, prep_grid, dim3(256), 0, st, static_cast<const _Float16*>(k),
-                     static_cast<const _Float16*>(v), vt, kpad, (int)p->seq_k, (int)lay.nk_pad);
+                     static_cast<const _Float16*>(v), vt, kpad, (int)p->seq_k, (int)lay.nk_pad,
+                     (int)p->heads_kv, ks, vs);
   if (hipGetLastError() != hipSuccess) return FA_ERR_LAUNCH;
 
   FaArgs args;
@@ -1116,6 +1162,9 @@ int launch(const fa_problem* p, const void* q, const void* k, const void* v, voi
   args.causal = p->causal != FA_CAUSAL_NONE;
   args.causal_off = p->causal == FA_CAUSAL_BOTTOM_RIGHT ? (int)(p->seq_k - p->seq_q) : 0;
   args.c = (float)((double)p->scale * LOG2E);
+  args.qs = qs;
+  args.os = os;
+  args.ks = lay.pad_k ? contiguous(p->heads_kv, lay.nk_pad) : ks;
   const int64_t tiles_q = (p->seq_q + tile->rows - 1) / tile->rows;
   const unsigned grid = (unsigned)(p->batch * p->heads_q * tiles_q);
   attn_fn fn = stats ? (p->acc == FA_ACC_FP16 ? tile->fp16_capture : tile->fp32_capture)
@@ -1164,12 +1213,19 @@ int fa_fwd_select(const fa_problem* p, int32_t* kernel) {
 
 int fa_fwd(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
            void* workspace, uint64_t workspace_bytes, void* stream) {
-  return launch(p, q, k, v, o, nullptr, nullptr, 0, workspace, workspace_bytes, stream);
+  return launch(p, nullptr, q, k, v, o, nullptr, nullptr, 0, workspace, workspace_bytes, stream);
 }
 
 int fa_fwd_lse(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
                float* lse, void* workspace, uint64_t workspace_bytes, void* stream) {
-  return launch(p, q, k, v, o, lse, nullptr, 0, workspace, workspace_bytes, stream);
+  return launch(p, nullptr, q, k, v, o, lse, nullptr, 0, workspace, workspace_bytes, stream);
+}
+
+int fa_fwd_strided(const fa_problem* p, const fa_strides* strides, const void* q, const void* k,
+                   const void* v, void* o, float* lse, void* workspace, uint64_t workspace_bytes,
+                   void* stream) {
+  if (!strides) return FA_ERR_NULL;
+  return launch(p, strides, q, k, v, o, lse, nullptr, 0, workspace, workspace_bytes, stream);
 }
 
 int fa_fwd_capture_count(const fa_problem* p, uint64_t* count, int32_t* block_keys) {
@@ -1187,7 +1243,7 @@ int fa_fwd_capture(const fa_problem* p, const void* q, const void* k, const void
                    float* lse, float* stats, uint64_t stats_count, void* workspace,
                    uint64_t workspace_bytes, void* stream) {
   if (!stats) return FA_ERR_NULL;
-  return launch(p, q, k, v, o, lse, stats, stats_count, workspace, workspace_bytes, stream);
+  return launch(p, nullptr, q, k, v, o, lse, stats, stats_count, workspace, workspace_bytes, stream);
 }
 
 int fa_kernel_count(void) { return kNumTiles; }

@@ -111,6 +111,29 @@ int fa_fwd_lse(const fa_problem* p, const void* q, const void* k, const void* v,
                float* lse, void* workspace, uint64_t workspace_bytes, void* stream);
 
 /*
+ * Element strides of dims B, H and N of q, k, v and o (dim D, the 128
+ * head dimensions, must be contiguous): a [B, H, N, 128] view of any layout
+ * whose rows are 16-byte aligned, e.g. the sequence-major [B, N, H, 128]
+ * tensors FlashAttention-style code produces, whose b, h, n strides are
+ * N*H*128, 128 and H*128. Every stride is a non-negative multiple of 8 and
+ * the n stride is at least 128. The reference accepts contiguous BNSD
+ * tensors only (FP32V/binding.py:89-99); this is an addition.
+ */
+typedef struct fa_strides {
+  int64_t q[3], k[3], v[3], o[3];
+} fa_strides;
+
+/*
+ * fa_fwd_lse() on strided q, k, v and o (lse stays contiguous [B, Hq, Nq],
+ * NULL for none). Same workspace as fa_fwd(); FA_ERR_ALIGN for strides that
+ * are not multiples of 8, FA_ERR_GEOMETRY for negative strides, row strides
+ * below 128 or a key row span of 2^31 bytes or more.
+ */
+int fa_fwd_strided(const fa_problem* p, const fa_strides* strides, const void* q, const void* k,
+                   const void* v, void* o, float* lse, void* workspace, uint64_t workspace_bytes,
+                   void* stream);
+
+/*
  * Capture (debug) mode: fa_fwd_lse() that also records the online-softmax
  * statistics of every query row after every key block of the selected tile,
  * the counterpart of the reference's capture flag, which dumps the running

@@ -628,3 +628,71 @@ def test_custom_scale(library_path, scale, causal):
         torch.cuda.synchronize()
         check(out.float().cpu().numpy(), exact, acc, f"scale {scale}", wabs)
         check_lse(lse.cpu().numpy(), exact_lse, f"scale {scale} {acc}")
+
+
+# --------------------------------------------------------------------------- #
+# strided layouts (fa_fwd_strided)
+# --------------------------------------------------------------------------- #
+STRIDED = [(2, 12, 1, 512, 512), (1, 6, 2, 300, 1000), (1, 4, 4, 1000, 129)]
+
+
+@pytest.mark.parametrize("causal", ["none", "top_left"])
+@pytest.mark.parametrize("b,hq,hkv,nq,nk", STRIDED)
+def test_sequence_major_views_match_contiguous(library_path, b, hq, hkv, nq, nk, causal):
+    """[B, N, H, 128] tensors viewed as [B, H, N, 128] (no copy) give bitwise
+    the result of their contiguous copies, and match the oracle."""
+    say(f"case strided BSHD B{b} Hq{hq} Hkv{hkv} nq={nq} nk={nk} causal={causal}")
+    g = torch.Generator().manual_seed(nq * 3 + nk)
+    qs = torch.randn(b, nq, hq, 128, generator=g, dtype=torch.float16).cuda()
+    ks = torch.randn(b, nk, hkv, 128, generator=g, dtype=torch.float16).cuda()
+    vs = torch.randn(b, nk, hkv, 128, generator=g, dtype=torch.float16).cuda()
+    q, k, v = (t.transpose(1, 2) for t in (qs, ks, vs))
+    assert not q.is_contiguous()
+    exact = orc.attention_f64(q.cpu(), k.cpu(), v.cpu(), causal=causal)
+    for acc in ("fp32", "fp16"):
+        op = Operator(library_path, AttentionConfig(acc=acc, causal=causal))
+        out_s, lse_s = op(q, k, v, return_lse=True)
+        out_s, lse_s = out_s.clone(), lse_s.clone()
+        out_c, lse_c = op(q.contiguous(), k.contiguous(), v.contiguous(), return_lse=True)
+        torch.cuda.synchronize()
+        assert bool(torch.equal(out_s, out_c)) and bool(torch.equal(lse_s, lse_c)), acc
+        check(out_s.float().cpu().numpy(), exact, acc, f"strided {causal}")
+
+
+@pytest.mark.parametrize("kernel", kernel_ids())
+def test_padded_rows_and_broadcast_heads_every_tile(library_path, kernel):
+    """Rows padded to 136 elements, and K/V heads broadcast with stride 0
+    (expand), through every tile configuration."""
+    rows, keys = tile_of(kernel)
+    nq, nk = 2 * rows, 4 * keys
+    say(f"case strided padded/broadcast tile {kernel} nq={nq} nk={nk}")
+    g = torch.Generator().manual_seed(kernel)
+    qp = torch.randn(1, 4, nq, 136, generator=g, dtype=torch.float16).cuda()
+    kp = torch.randn(1, 1, nk, 136, generator=g, dtype=torch.float16).cuda()
+    vp = torch.randn(1, 1, nk, 136, generator=g, dtype=torch.float16).cuda()
+    q, k1, v1 = qp[..., :128], kp[..., :128], vp[..., :128]
+    k2, v2 = k1.expand(1, 2, nk, 128), v1.expand(1, 2, nk, 128)   # Hkv = 2 sharing one head
+    for acc in ("fp32", "fp16"):
+        op = Operator(library_path, AttentionConfig(acc=acc, kernel=kernel))
+        a = op(q, k2, v2).clone()
+        ref = op(q.contiguous(), k2.contiguous(), v2.contiguous()).clone()
+        torch.cuda.synchronize()
+        assert bool(torch.equal(a, ref)), (kernel, acc)
+    exact = orc.attention_f64(q.cpu(), k2.cpu(), v2.cpu())
+    check(a.float().cpu().numpy(), exact, "fp16", "strided padded")
+
+
+def test_strided_rejections(library_path):
+    say("case strided rejections")
+    op = Operator(library_path, AttentionConfig())
+    base = torch.randn(1, 2, 256, 136, dtype=torch.float16).cuda()
+    k = torch.randn(1, 1, 256, 128, dtype=torch.float16).cuda()
+    with pytest.raises(ValueError):                       # last dimension not contiguous
+        wide = torch.randn(1, 2, 256, 272, dtype=torch.float16).cuda()
+        op(torch.as_strided(wide, (1, 2, 256, 128), (2 * 256 * 272, 256 * 272, 272, 2)), k, k)
+    flat = torch.zeros(2 * 256 * 136 + 8, dtype=torch.float16).cuda()
+    with pytest.raises(ValueError):                       # rows not 16-byte aligned
+        op(flat[4:4 + 2 * 256 * 136].view(1, 2, 256, 136)[..., :128], k, k)
+    cap = Operator(library_path, AttentionConfig(capture=True))
+    with pytest.raises(ValueError):                       # capture needs contiguous inputs
+        cap(base[..., :128], k, k)

@@ -204,3 +204,26 @@ def test_operator_validation_without_gpu(library_path):
         plain(q[:, :, :200], k, k)
     with pytest.raises(ValueError):
         binding.AttentionConfig(acc="bf16")
+
+
+def test_strided_validation(lib):
+    # Layout errors are reported before anything is launched.
+    prob = problem(heads_q=4, seq_q=256, seq_k=256)
+    fake = C.c_void_p(256)
+
+    def call(**over):
+        st = binding.FaStrides()
+        vals = dict(q=(4 * 256 * 128, 256 * 128, 128), k=(256 * 128, 256 * 128, 128),
+                    v=(256 * 128, 256 * 128, 128), o=(4 * 256 * 128, 256 * 128, 128))
+        vals.update(over)
+        for name, t in vals.items():
+            getattr(st, name)[:] = t
+        return lib.fa_fwd_strided(C.byref(prob), C.byref(st), fake, fake, fake, fake, None, fake,
+                                  1 << 30, None)
+
+    assert lib.fa_fwd_strided(C.byref(prob), None, fake, fake, fake, fake, None, fake, 1 << 30,
+                              None) == 1
+    assert call(q=(4 * 256 * 128, 256 * 128, 132)) == 5          # row stride not a multiple of 8
+    assert call(k=(256 * 128, -8, 128)) == 2                     # negative stride
+    assert call(o=(4 * 256 * 128, 256 * 128, 64)) == 2           # rows overlap
+    assert call(k=(0, 0, 1 << 23), v=(0, 0, 128)) == 2           # key rows span >= 2^31 bytes

@@ -696,3 +696,60 @@ def test_strided_rejections(library_path):
     cap = Operator(library_path, AttentionConfig(capture=True))
     with pytest.raises(ValueError):                       # capture needs contiguous inputs
         cap(base[..., :128], k, k)
+
+
+# --------------------------------------------------------------------------- #
+# streams and graph capture (the C ABI allocates nothing and keeps no state)
+# --------------------------------------------------------------------------- #
+def test_concurrent_streams_independent(library_path):
+    """Two problems on two streams with their own operators (workspaces)
+    overlap without interfering: each equals its serial result."""
+    say("case two streams")
+    g = torch.Generator().manual_seed(21)
+    a = [torch.randn(1, 12, 2048, 128, generator=g, dtype=torch.float16).cuda()] + \
+        [torch.randn(1, 1, 2048, 128, generator=g, dtype=torch.float16).cuda() for _ in range(2)]
+    b = [torch.randn(2, 4, 1000, 128, generator=g, dtype=torch.float16).cuda()] + \
+        [torch.randn(2, 2, 3000, 128, generator=g, dtype=torch.float16).cuda() for _ in range(2)]
+    op_a = Operator(library_path, AttentionConfig())
+    op_b = Operator(library_path, AttentionConfig(acc="fp16", causal="top_left"))
+    ref_a = op_a(*a).clone()
+    ref_b = op_b(*b).clone()
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            out_a = op_a(*a)
+        with torch.cuda.stream(s2):
+            out_b = op_b(*b)
+        torch.cuda.synchronize()
+        assert bool(torch.equal(out_a, ref_a)) and bool(torch.equal(out_b, ref_b))
+
+
+def test_graph_capture_replays(library_path):
+    """fa_fwd captured in a HIP graph: every replay (with eager work and
+    synchronisation in between, inputs changed in place) equals the eager
+    result for the current inputs."""
+    say("case graph capture")
+    g = torch.Generator().manual_seed(22)
+    q = torch.randn(1, 12, 1024, 128, generator=g, dtype=torch.float16).cuda()
+    k = torch.randn(1, 1, 1024, 128, generator=g, dtype=torch.float16).cuda()
+    v = torch.randn(1, 1, 1024, 128, generator=g, dtype=torch.float16).cuda()
+    op = Operator(library_path, AttentionConfig())
+    op(q, k, v)                                   # allocates the cached output and workspace
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            out = op(q, k, v)
+    torch.cuda.synchronize()
+    eager = Operator(library_path, AttentionConfig())
+    for rep in range(4):
+        q.copy_(torch.randn(q.shape, generator=g, dtype=torch.float16).cuda())
+        v.mul_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = eager(q, k, v)
+        torch.cuda.synchronize()
+        assert bool(torch.equal(out, want)), rep

@@ -30,9 +30,11 @@
 // Online softmax in base 2 with the scale folded in (c = scale*log2(e)):
 //   m' = max(m, rowmax(S)),  alpha = 2^((m - m') c),  P = 2^(S c - m' c),
 //   l' = alpha l + rowsum(P16),  O' = alpha O + P16 V
-// where P16 is P rounded to FP16 (the MFMA operand) and the row sum is taken
-// over the same rounded values, so numerator and denominator use identical
-// weights. Semantics follow the reference's FP32 vector softmax
+// where P16 is P rounded to FP16 (the MFMA operand). With the FP32 O the row
+// sum is taken over the same rounded values, so numerator and denominator
+// use identical weights; with the FP16 O it is taken over the unrounded FP32
+// P (cheaper there; the difference is within 2^-11 relative per term).
+// Semantics follow the reference's FP32 vector softmax
 // (project/op_kernel/online_softmax.h:86-224, vector_output.h:22-86 of the
 // FP32 variant) and, for FA_ACC_FP16, its FP16-O merge (vector_output.h:
 // 130-210 of backends/cce_fa_nqkq_nz_resident_v13_q768_pool_i4_p128).
@@ -789,7 +791,11 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
     }
     alpha_prev = alpha;
     const float mc = m * c;
-    // Row sum of the rounded P in four independent partial sums.
+    // Row sum in four independent partial sums. The FP32 accumulator sums
+    // the FP16-rounded P the PV products use (one dot per pair); the FP16
+    // accumulator, whose softmax step is the longer of its two, sums the
+    // unrounded FP32 P with two adds (measured 3% faster there, 6% slower
+    // for the FP32 accumulator).
     float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
@@ -803,7 +809,8 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
           const h2 pr = {(_Float16)p0, (_Float16)p1};
           frag[e] = pr[0];
           frag[e + 1] = pr[1];
-          ls[e >> 1] = __builtin_amdgcn_fdot2(pr, ones, ls[e >> 1], false);
+          if constexpr (ACC16) ls[e >> 1] += p0 + p1;
+          else ls[e >> 1] = __builtin_amdgcn_fdot2(pr, ones, ls[e >> 1], false);
         }
         p[2 * t + g2] = frag;
       }

@@ -13,13 +13,19 @@ peak): ``value`` = QK/PV TFLOP/s, ``ms_per_step`` = forward milliseconds,
 ``roofline`` against MI355X's dense FP16 MFMA peak (``traffic`` = HBM bytes
 per attention launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
 summary for the same workload and tile, null when there is none), and
-``cpu_baseline`` = the canonical FP32 formula timed on the host cores over a
-bounded sample of the same workload (a few query rows of head 0 against all
-keys; the oracle's CPU restatement, a reported baseline only).
+``cpu_baseline`` = the canonical FP32 formula (the oracle's CPU
+restatement) timed on every host core over the full c0 forward, the
+CPU-runnable plumbing configuration (a reported baseline only).
 
 ``--causal top_left|bottom_right`` times the same workload under a causal
 mask (not the headline metric): FLOPs then count only the (query, key)
 pairs the mask leaves, 4*B*Hq*D*pairs.
+
+``clock`` (HIP backends) is the shader clock the attention kernel ran at,
+from one trace-mode forward after the timed region, with the MFMA roof at
+that clock; ``sustained`` is the board's sustained dense FP16 matrix rate
+measured in the same process (torch FP16 GEMMs and an MFMA-only loop,
+``fa_amd.measure.ceiling``), with ``value`` as a fraction of each.
 
 ``--copy-mib M`` additionally runs ``--copy-reps`` plain device-to-device
 copies of M MiB after the timed region, untimed: the calibration kernel the
@@ -56,10 +62,12 @@ def parse_args(argv=None):
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
-                   help="approximate CPU time budget of the baseline sample")
+                   help="host time budget of the CPU baseline's timed runs")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="after timing, run plain copies of this many MiB (counter calibration)")
     p.add_argument("--copy-reps", type=int, default=3)
+    p.add_argument("--no-ceiling", action="store_true",
+                   help="skip the sustained-rate (GEMM and MFMA loop) and clock measurements")
     return p.parse_args(argv)
 
 
@@ -87,47 +95,48 @@ def traffic_from_profiles(workload_key):
     return None
 
 
-def cpu_baseline(case, cpu, budget_s):
-    """Time the oracle's canonical FP32 formula on a sample of the workload.
+def cpu_baseline(min_runs=5, budget_s=12.0):
+    """Time the canonical FP32 formula on the host for the full c0 forward.
 
-    The sample is the first R query rows of (batch 0, head 0) against every
-    key of that batch -- the same per-row work as the full problem, which is
-    a sum of independent rows. R is sized from a probe run so that five or
-    more timed runs fill about ``budget_s`` seconds of host time.
+    The CPU-runnable plumbing configuration c0 (B=1, Hq=12, Hkv=1, N=4096,
+    D=128, 1.03e11 FLOP) run whole through ``oracle.attention_f32`` (the
+    canonical ``softmax(q k^T * scale) v`` in FP32 torch on the CPU) with
+    ``torch.set_num_threads(os.cpu_count())``: one warmup run, then the
+    median of at least ``min_runs`` runs (more while they fit in
+    ``budget_s`` seconds, at most 25). A reported baseline, not a target.
     """
     import torch
 
+    from fa_amd.problem.canonical import build_canonical
+    from fa_amd.problem.cases import CASES, CPU_CASE
     from oracle.attention import attention_f32
 
-    k, v = cpu["k"][:1, :1], cpu["v"][:1, :1]
-    nk, d = k.shape[2], k.shape[3]
-    cores = torch.get_num_threads()
-
-    def run(rows):
-        q = cpu["q"][:1, :1, :rows]
-        t0 = time.perf_counter()
-        attention_f32(q, k, v)
-        return time.perf_counter() - t0
-
-    probe_rows = 16
-    run(probe_rows)                                # warmup
-    per_row = run(probe_rows) / probe_rows
-    rows = int(max(16, min(cpu["q"].shape[2], budget_s / 6 / per_row)) // 16 * 16)
-    times = []
-    start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - start < budget_s and len(times) < 50):
-        times.append(run(rows))
+    case = CASES[CPU_CASE]
+    cores = os.cpu_count() or 1
+    threads_before = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        x = build_canonical(case, seed=0)
+        attention_f32(x["q"], x["k"], x["v"])               # warmup
+        times = []
+        start = time.perf_counter()
+        while len(times) < min_runs or (time.perf_counter() - start < budget_s and len(times) < 25):
+            t0 = time.perf_counter()
+            attention_f32(x["q"], x["k"], x["v"])
+            times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(threads_before)
     med = statistics.median(times)
-    flops = 4.0 * rows * nk * d
     return {
-        "value": round(flops / med / 1e12, 5),
+        "value": round(case.flops / med / 1e12, 5),
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
         "ms": round(med * 1e3, 2),
-        "sample": f"{case.name}: {rows} query rows of batch 0 / head 0 against all {nk} keys "
-                  f"(oracle.attention_f32, torch CPU FP32), median of {len(times)} runs "
-                  f"after 1 warmup",
+        "gflops": round(case.flops / med / 1e9, 1),
+        "sample": f"c0 {case.name}: the full forward ({case.flops:.3e} FLOP) through "
+                  f"oracle.attention_f32 (torch CPU FP32, {cores} threads), median of "
+                  f"{len(times)} runs after 1 warmup",
     }
 
 
@@ -141,7 +150,7 @@ def main(argv=None):
 
     import torch
 
-    from fa_amd.core import registry
+    from fa_amd.harness.catalog import Catalog
     from fa_amd.problem.canonical import build_canonical
     from fa_amd.problem.cases import CASES, visible_pairs
 
@@ -149,28 +158,21 @@ def main(argv=None):
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     case = CASES[args.case]
-    spec = registry.get(args.backend)
-    bind = registry.prepare_call(spec, case)
-    cpu = build_canonical(case, args.seed)
-    canonical = {name: t.to("cuda") for name, t in cpu.items()}
-    if args.no_cpu_baseline:
-        cpu = None
-    else:                                      # keep only what the CPU sample reads
-        cpu = {"q": cpu["q"][:1, :1].clone(), "k": cpu["k"][:1, :1].clone(),
-               "v": cpu["v"][:1, :1].clone()}
+    catalog = Catalog.default()
+    entry = catalog.attention(args.backend)
+    bind = catalog.prepare(args.backend, case)
+    canonical = build_canonical(case, args.seed, device="cuda")
     call = bind(canonical)
 
     from fa_amd.backends import hip_common
-    from fa_amd.binding import AttentionConfig, Operator
 
-    acc = getattr(spec, "ACC", None)
+    acc = getattr(entry.module, "ACC", None)
     tile_name = None
     if acc is None and args.causal != "none":
         print(f"--causal needs a HIP backend, not {args.backend}", file=sys.stderr)
         return 2
     if acc is not None:
-        op = Operator(hip_common.project(case, prebuilt=True).artifact_paths()[0],
-                      AttentionConfig(acc=acc, kernel=args.kernel, causal=args.causal))
+        op = hip_common.operator(acc, case, kernel=args.kernel, causal=args.causal)
         tile_name = op.kernel_name(canonical["q"].shape, canonical["k"].shape)
         if args.kernel or args.causal != "none":
             # Explicit tile configuration (tuning runs) or a causal mask.
@@ -201,6 +203,29 @@ def main(argv=None):
             torch.bitwise_not(src, out=dst)
         torch.cuda.synchronize()
         del src, dst
+
+    # After the timed region (untimed): the running clock from one trace-mode
+    # forward of the same tile, and the board's sustained matrix rate.
+    clock_line, sustained = None, None
+    if not args.no_ceiling:
+        from fa_amd.measure import ceiling, clock
+
+        if acc is not None:
+            traced = hip_common.operator(acc, case, kernel=args.kernel, causal=args.causal,
+                                         trace=True)
+            traced(canonical["q"], canonical["k"], canonical["v"])
+            torch.cuda.synchronize()
+            s = clock.summarize(traced.last["trace"].cpu().numpy())
+            f = s["mean_mhz_time_weighted"]
+            clock_line = {"median_mhz": round(s["median_mhz"], 1), "mean_mhz": round(f, 1),
+                          "p10_mhz": round(s["p10_mhz"], 1), "p90_mhz": round(s["p90_mhz"], 1),
+                          "mfma_roof_at_clock": round(clock.roof_at(f), 1),
+                          "frac_at_clock": round(tflops / clock.roof_at(f), 4),
+                          "source": "fa_fwd_trace records (s_memtime / s_memrealtime per workgroup)"}
+            del traced
+        sustained = ceiling.measure(gemm_reps=10)
+        sustained["frac_of_gemm"] = round(tflops / sustained["gemm_best_tflops"], 4)
+        sustained["frac_of_mfma_loop"] = round(tflops / sustained["mfma_loop_best_tflops"], 4)
 
     workload_key = f"{args.backend} c{args.case} {case.name} tile={tile_name}"
     if args.causal != "none":
@@ -238,7 +263,9 @@ def main(argv=None):
             "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
             "traffic": traffic_from_profiles(workload_key),
         },
-        "cpu_baseline": None if cpu is None else cpu_baseline(case, cpu, args.cpu_seconds),
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(budget_s=args.cpu_seconds),
+        "clock": clock_line,
+        "sustained": sustained,
     }
     print(json.dumps(line), flush=True)
     return 0

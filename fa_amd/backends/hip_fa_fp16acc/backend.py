@@ -10,7 +10,7 @@ reference's ``cce_fa_nqkq_nz_resident_v13_q768_pool_i4_p128``
 """
 
 from fa_amd.backends import hip_common
-from fa_amd.core.contract import Meta
+from fa_amd.harness.contract import Meta
 
 META = Meta(
     name="hip_fa_fp16acc",
@@ -23,12 +23,8 @@ META = Meta(
 ACC = "fp16"
 
 
-def project(case):
-    return hip_common.project(case)
-
-
-def load(case, project):
-    return hip_common.load(ACC, case, project)
+def operator(case):
+    return hip_common.operator(ACC, case)
 
 
 def adapt(case, canonical):

@@ -9,7 +9,7 @@ reference's ``cce_fa_nk_nz_vector_fp32_v5_sumpack``
 """
 
 from fa_amd.backends import hip_common
-from fa_amd.core.contract import Meta
+from fa_amd.harness.contract import Meta
 
 META = Meta(
     name="hip_fa_fp32acc",
@@ -22,12 +22,8 @@ META = Meta(
 ACC = "fp32"
 
 
-def project(case):
-    return hip_common.project(case)
-
-
-def load(case, project):
-    return hip_common.load(ACC, case, project)
+def operator(case):
+    return hip_common.operator(ACC, case)
 
 
 def adapt(case, canonical):

@@ -10,7 +10,7 @@ the query rows in chunks so an N = 131072 problem never materialises N^2
 scores at once.
 """
 
-from fa_amd.core.contract import Meta
+from fa_amd.harness.contract import Meta
 
 META = Meta(
     name="torch_ref",

@@ -31,6 +31,8 @@ FA_ACC = {"fp32": 0, "fp16": 1}
 # scaled_dot_product_attention(is_causal=True)) or bottom-right
 # (j <= i + Nk - Nq).
 FA_CAUSAL = {"none": 0, "top_left": 1, "bottom_right": 2}
+# 64-bit words per workgroup record of trace mode (fa_fwd_trace).
+TRACE_WORDS = 8
 
 
 class FaProblem(C.Structure):
@@ -69,6 +71,10 @@ SIGNATURES = {
     "fa_fwd_capture": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p,
                                  C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p,
                                  C.c_uint64, C.c_void_p]),
+    "fa_fwd_trace_count": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_uint64)]),
+    "fa_fwd_trace": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p,
+                               C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64,
+                               C.c_void_p]),
     "fa_fwd_tile": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "fa_fwd_select": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32)]),
     "fa_kernel_count": (C.c_int, []),
@@ -92,13 +98,15 @@ class AttentionConfig:
     """Launch configuration: accumulation variant, tile selector (0 = automatic),
     capture (debug) mode, which records every row's online-softmax
     statistics per key block (the reference config's ``capture`` flag,
-    ``backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/backend.py:27``), and the
+    ``backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/backend.py:27``), the
     attention mask (``FA_CAUSAL``; a row that sees no key gets O = 0 and
-    lse = -inf)."""
+    lse = -inf), and trace mode, which records per workgroup where it ran
+    and its clock stamps (the reference kernel's ``trace`` output)."""
     acc: str = "fp32"
     kernel: int = 0
     capture: bool = False
     causal: str = "none"
+    trace: bool = False
 
     def __post_init__(self):
         if self.acc not in FA_ACC:
@@ -109,6 +117,10 @@ class AttentionConfig:
             raise ValueError("capture must be a bool")
         if self.causal not in FA_CAUSAL:
             raise ValueError(f"unknown causal mode {self.causal!r}")
+        if not isinstance(self.trace, bool):
+            raise ValueError("trace must be a bool")
+        if self.trace and self.capture:
+            raise ValueError("capture and trace are separate kernels; pick one")
 
 
 def make_problem(q_shape, k_shape, scale, config):
@@ -165,8 +177,6 @@ class Operator:
         rows, keys = self.tile(q.shape, k.shape)
         if nq % rows or k.shape[2] % keys or max(nq, k.shape[2]) >= 2 ** 30:
             raise ValueError(f"unsupported query/key tail (Nq % {rows}, Nk % {keys})")
-        if self.config.causal != "none" and (rows, keys) != (1, 1):
-            raise ValueError("a causal mask needs a masking tile (kernel 0 or a ping-pong tile)")
         for t in (q, k, v):
             if t.device.type != "cuda" or t.device != q.device or t.dtype != torch.float16:
                 raise ValueError("Q/K/V must be FP16 on the same GPU")
@@ -207,6 +217,17 @@ class Operator:
             self.buffers[key] = (stats, block.value)
         return self.buffers[key]
 
+    def trace_for(self, q, k, prob):
+        import torch
+
+        key = (tuple(q.shape), tuple(k.shape), q.device, self.config, "trace")
+        if key not in self.buffers:
+            count = C.c_uint64()
+            self.check(self.lib.fa_fwd_trace_count(C.byref(prob), C.byref(count)), "trace")
+            self.buffers[key] = torch.empty((count.value // TRACE_WORDS, TRACE_WORDS),
+                                            dtype=torch.int64, device=q.device)
+        return self.buffers[key]
+
     def __call__(self, q, k, v, scale=None, return_lse=False):
         """O (cached tensor), or (O, lse) with ``return_lse``: lse [B, Hq, Nq] FP32
         natural-log log-sum-exp of the scaled scores of each query row.
@@ -214,7 +235,9 @@ class Operator:
         With ``config.capture`` the call also fills ``self.last["stats"]``,
         FP32 [4, nblk, B, Hq, Nq]: per key block of ``self.last["block_keys"]``
         keys, each row's running max m (natural-log units), running sum l
-        relative to m, rescale factor alpha and block sum z relative to m."""
+        relative to m, rescale factor alpha and block sum z relative to m.
+        With ``config.trace`` it fills ``self.last["trace"]``, int64
+        [workgroups, 8]: the per-workgroup records of ``fa_fwd_trace``."""
         import torch
 
         self.validate(q, k, v)
@@ -228,9 +251,10 @@ class Operator:
         capture = self.config.capture
         lse = self.buffers_for(q, k, lse=True) if (return_lse or capture) else None
         stats, block = self.stats_for(q, k, prob) if capture else (None, 0)
+        trace = self.trace_for(q, k, prob) if self.config.trace else None
         strided = not all(t.is_contiguous() for t in (q, k, v))
-        if strided and capture:
-            raise ValueError("capture mode needs contiguous Q/K/V")
+        if strided and (capture or trace is not None):
+            raise ValueError("capture and trace modes need contiguous Q/K/V")
         with torch.cuda.device(q.device):
             need = max(size.value, 16)
             if self.workspace is None or self.workspace.device != q.device \
@@ -250,13 +274,17 @@ class Operator:
             elif capture:
                 status = self.lib.fa_fwd_capture(C.byref(prob), *common, lse.data_ptr(),
                                                  stats.data_ptr(), stats.numel(), *tail)
+            elif trace is not None:
+                status = self.lib.fa_fwd_trace(C.byref(prob), *common, trace.data_ptr(),
+                                               trace.numel(), *tail)
             elif return_lse:
                 status = self.lib.fa_fwd_lse(C.byref(prob), *common, lse.data_ptr(), *tail)
             else:
                 status = self.lib.fa_fwd(C.byref(prob), *common, *tail)
             self.check(status, "launch")
-            extra = tuple(t for t in (lse, stats) if t is not None)
+            extra = tuple(t for t in (lse, stats, trace) if t is not None)
             for t in (q, k, v, out, self.workspace) + extra:
                 t.record_stream(stream)
-        self.last = {"output": out, "lse": lse, "stats": stats, "block_keys": block}
+        self.last = {"output": out, "lse": lse, "stats": stats, "block_keys": block,
+                     "trace": trace}
         return (out, lse) if return_lse else out

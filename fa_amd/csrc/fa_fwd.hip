@@ -43,6 +43,7 @@
 #include <stdint.h>
 #include <math.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "../../include/fa_hip.h"
@@ -65,15 +66,35 @@ constexpr float MASKED = -1.0e38f;
 constexpr double LOG2E = 1.4426950408889634;
 constexpr float LN2 = 0.6931471805599453f;
 
+// Kernel instantiation modes. Capture records the online-softmax statistics
+// of every row after every key block; trace records, per workgroup, where it
+// ran and two clock stamps around its key loop. Both are separate kernels.
+enum KernelMode { MODE_RUN = 0, MODE_CAPTURE = 1, MODE_TRACE = 2 };
+
+// Trace record of one workgroup (64-bit words, record index = blockIdx.x):
+//   0  hardware placement: HW_ID register (wave slot, SIMD, CU, shader array,
+//      shader engine) in bits 0-31, XCC_ID (the accelerator die, one of 8)
+//      in bits 32-35, both read by wave 0
+//   1  s_memrealtime at kernel entry (constant 100 MHz reference clock)
+//   2  s_memrealtime after the key loop (every wave past the final barrier)
+//   3  s_memtime at kernel entry (shader-clock cycles)
+//   4  s_memtime after the key loop
+//   5  blockIdx.x
+//   6  key blocks the workgroup streamed
+//   7  keys per block
+// The shader clock the workgroup ran at is (w4 - w3) / (w2 - w1) * 100 MHz.
+constexpr int TRACE_WORDS = 8;
+
 // Kernel arguments. seq_k is the key length of the K and V^T buffers the
 // kernel reads (a multiple of its key block); keys at or past nk_valid are
 // zero padding and masked out of the softmax. lse (FP32 [B, Hq, Nq],
 // natural-log log-sum-exp of the scaled scores) may be null. stats, when not
 // null, receives the online-softmax statistics of every row after every key
-// block (capture mode, ping-pong tiles): FP32 [4][seq_k / BN][B * Hq * Nq]
+// block (capture mode): FP32 [4][seq_k / BN][B * Hq * Nq]
 // holding the running max m (natural-log units, scale * score), the running
 // sum l relative to m, the rescale factor alpha applied at that block, and
-// the block's own row sum z relative to m. c is the softmax scale times
+// the block's own row sum z relative to m. trace, in trace mode, receives
+// one record of TRACE_WORDS 64-bit words per workgroup (see trace_record). c is the softmax scale times
 // log2(e). With causal set, query row i sees keys j <= i + causal_off only
 // (causal_off = 0 aligns the mask top-left, Nk - Nq bottom-right); a row that
 // sees no key gets O = 0 and lse = -inf. qs, ks and os are the element
@@ -89,6 +110,7 @@ struct FaArgs {
   _Float16* o;
   float* lse;
   float* stats;
+  uint64_t* trace;
   int heads_q, group, seq_q, seq_k, nk_valid;
   int causal, causal_off;
   float c;
@@ -99,15 +121,6 @@ struct FaArgs {
 template <typename T>
 __device__ __forceinline__ T* row_at(T* base, const Strides& st, int b, int h, int n) {
   return base + (int64_t)b * st.b + (int64_t)h * st.h + (int64_t)n * st.n;
-}
-
-// 16-byte chunk swizzle for an LDS tile whose rows are CPR chunks long.
-// Rows are read 32 at a time at one logical chunk column; the XOR spreads any
-// 16 consecutive rows over 16 distinct 16-byte bank groups (256 bytes).
-template <int CPR>
-__device__ __forceinline__ int swz(int row, int chunk) {
-  constexpr int RPW = 16 / CPR;       // rows sharing one 256-byte bank window
-  return chunk ^ ((row / RPW) & (CPR - 1));
 }
 
 // Maximum of two scores. IEEE-754 maximum (NaN-propagating) lowers to a
@@ -181,243 +194,6 @@ __global__ void __launch_bounds__(256) fa_prep_kernel(const _Float16* __restrict
   }
 }
 
-// The attention body. ACC16 selects the FP16 O accumulator; NW waves per
-// workgroup, SUB 32-row subtiles per wave, BN keys per block.
-// Requires Nq % BM == 0 and Nk % BN == 0 (no masked tail) and no causal mask.
-template <bool ACC16, int NW, int SUB, int BN>
-__device__ __forceinline__ void fa_fwd_body(const FaArgs& args) {
-  const _Float16* __restrict__ q = args.q;
-  const _Float16* __restrict__ k = args.k;
-  const _Float16* __restrict__ vt = args.vt;
-  _Float16* __restrict__ o = args.o;
-  const int heads_q = args.heads_q, group = args.group, seq_q = args.seq_q, seq_k = args.seq_k;
-  const float c = args.c;
-  constexpr int NT = NW * 64;
-  constexpr int BM = NW * SUB * 32;
-  constexpr int KT = BN / 32;          // 32-key S^T tiles per block
-  constexpr int KS = BN / 16;          // 16-key PV steps per block
-  constexpr int KCH = BN * 16;         // 16-byte chunks in a K block (BN rows x 256 B)
-  constexpr int VCPR = BN / 8;         // chunks per V^T row (BN keys)
-  constexpr int VCH = HD * VCPR;       // chunks in a V^T block
-  constexpr int KLD = KCH / NT;        // K chunks each thread stages per block
-  constexpr int VLD = VCH / NT;
-  static_assert(KCH % NT == 0 && VCH % NT == 0, "block must split evenly over threads");
-  static_assert(BN % 32 == 0, "BN must be a multiple of 32");
-
-  __shared__ u32x4 smem[2][KCH + VCH];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hf = lane >> 5;
-
-  const int tiles_q = seq_q / BM;
-  const int bh = blockIdx.x / tiles_q;
-  const int qt = blockIdx.x - bh * tiles_q;
-  const int b = bh / heads_q, h = bh - b * heads_q;
-  const int heads_kv = heads_q / group;
-  const size_t kv = (size_t)b * heads_kv + h / group;
-  const _Float16* kp = row_at(k, args.ks, b, h / group, 0);
-  const _Float16* vp = vt + kv * (size_t)HD * seq_k;
-  const int rw0 = qt * BM + wave * (SUB * 32);   // this wave's first query row in (b, h)
-  const size_t row0 = (size_t)bh * seq_q + rw0;   // its index in [B * Hq * Nq] (lse)
-
-  // Q^T operand fragments: lane holds query row l32, dims 16kk+8hf..+7.
-  h8 qf[SUB][8];
-#pragma unroll
-  for (int u = 0; u < SUB; ++u)
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-      qf[u][kk] = *reinterpret_cast<const h8*>(row_at(q, args.qs, b, h, rw0 + u * 32 + l32) +
-                                               kk * 16 + hf * 8);
-
-  u32x4 kreg[KLD], vreg[VLD];
-  auto gload = [&](int blk) {
-    const int key0 = blk * BN;
-#pragma unroll
-    for (int j = 0; j < KLD; ++j) {
-      const int i = tid + j * NT;
-      const int r = i >> 4, ch = i & 15;
-      kreg[j] = *reinterpret_cast<const u32x4*>(kp + (int64_t)(key0 + r) * args.ks.n + ch * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < VLD; ++j) {
-      const int i = tid + j * NT;
-      const int d = i / VCPR, ch = i % VCPR;
-      vreg[j] = *reinterpret_cast<const u32x4*>(vp + (size_t)d * seq_k + key0 + ch * 8);
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < KLD; ++j) {
-      const int i = tid + j * NT;
-      const int r = i >> 4, ch = i & 15;
-      smem[buf][r * 16 + swz<16>(r, ch)] = kreg[j];
-    }
-#pragma unroll
-    for (int j = 0; j < VLD; ++j) {
-      const int i = tid + j * NT;
-      const int d = i / VCPR, ch = i % VCPR;
-      smem[buf][KCH + d * VCPR + swz<VCPR>(d, ch)] = vreg[j];
-    }
-  };
-
-  f32x16 acc[SUB][4];                  // FP32 O^T: dims 32dt.., queries l32
-  h2 acc16[SUB][4][8];                 // FP16 O^T, same element order, packed in pairs
-  float m[SUB], lsum[SUB];
-#pragma unroll
-  for (int u = 0; u < SUB; ++u) {
-    m[u] = NEG_BIG;
-    lsum[u] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      if constexpr (ACC16) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc16[u][dt][i] = h2{(_Float16)0.f, (_Float16)0.f};
-      } else {
-        acc[u][dt] = f32x16{};
-      }
-    }
-  }
-  const h2 ones = {(_Float16)1.f, (_Float16)1.f};
-
-  gload(0);
-  lstore(0);
-  __syncthreads();
-
-  const int nblk = seq_k / BN;
-  for (int n = 0; n < nblk; ++n) {
-    const int buf = n & 1;
-    if (n + 1 < nblk) gload(n + 1);
-    const u32x4* kb = smem[buf];
-    const u32x4* vb = smem[buf] + KCH;
-
-    // S^T = K Q^T
-    f32x16 s[SUB][KT];
-#pragma unroll
-    for (int u = 0; u < SUB; ++u)
-#pragma unroll
-      for (int t = 0; t < KT; ++t) s[u][t] = f32x16{};
-#pragma unroll
-    for (int t = 0; t < KT; ++t) {
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const int r = t * 32 + l32;
-        const h8 a = __builtin_bit_cast(h8, kb[r * 16 + swz<16>(r, 2 * kk + hf)]);
-#pragma unroll
-        for (int u = 0; u < SUB; ++u) s[u][t] = mfma32(a, qf[u][kk], s[u][t]);
-      }
-    }
-
-    // Online softmax, one query row per lane pair.
-    h8 p[SUB][KS];
-    float alpha[SUB];
-#pragma unroll
-    for (int u = 0; u < SUB; ++u) {
-      float mx = s[u][0][0];
-#pragma unroll
-      for (int t = 0; t < KT; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = smax(mx, s[u][t][r]);
-      mx = half_max(mx);
-      const float mnew = smax(m[u], mx);
-      alpha[u] = __builtin_amdgcn_exp2f((m[u] - mnew) * c);
-      m[u] = mnew;
-      const float mc = mnew * c;
-      float ls = 0.f;
-#pragma unroll
-      for (int t = 0; t < KT; ++t) {
-#pragma unroll
-        for (int g2 = 0; g2 < 2; ++g2) {
-          h8 frag;
-#pragma unroll
-          for (int e = 0; e < 8; e += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][t][8 * g2 + e], c, -mc));
-            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][t][8 * g2 + e + 1], c, -mc));
-            const h2 pr = {(_Float16)p0, (_Float16)p1};
-            frag[e] = pr[0];
-            frag[e + 1] = pr[1];
-            ls = __builtin_amdgcn_fdot2(pr, ones, ls, false);
-          }
-          p[u][2 * t + g2] = frag;
-        }
-      }
-      lsum[u] = lsum[u] * alpha[u] + ls;
-      if constexpr (!ACC16) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) acc[u][dt] *= alpha[u];
-      }
-    }
-
-    // O^T += V^T P^T
-    if constexpr (!ACC16) {
-#pragma unroll
-      for (int st = 0; st < KS; ++st) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          const int r = dt * 32 + l32;
-          const h8 a = __builtin_bit_cast(h8, vb[r * VCPR + swz<VCPR>(r, 2 * st + hf)]);
-#pragma unroll
-          for (int u = 0; u < SUB; ++u) acc[u][dt] = mfma32(a, p[u][st], acc[u][dt]);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        f32x16 part[SUB];
-#pragma unroll
-        for (int u = 0; u < SUB; ++u) part[u] = f32x16{};
-#pragma unroll
-        for (int st = 0; st < KS; ++st) {
-          const int r = dt * 32 + l32;
-          const h8 a = __builtin_bit_cast(h8, vb[r * VCPR + swz<VCPR>(r, 2 * st + hf)]);
-#pragma unroll
-          for (int u = 0; u < SUB; ++u) part[u] = mfma32(a, p[u][st], part[u]);
-        }
-        // O16 = alpha * O16 + fp16(partial), the FP16-O merge.
-#pragma unroll
-        for (int u = 0; u < SUB; ++u) {
-          const _Float16 a16 = (_Float16)alpha[u];
-          const h2 a2 = {a16, a16};
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const h2 pv = {(_Float16)part[u][2 * i], (_Float16)part[u][2 * i + 1]};
-            acc16[u][dt][i] = acc16[u][dt][i] * a2 + pv;
-          }
-        }
-      }
-    }
-
-    if (n + 1 < nblk) lstore(buf ^ 1);
-    __syncthreads();
-  }
-
-  // Epilogue: O / l -> FP16 (lane holds dims 32dt + 8g + 4hf + (0..3)), and
-  // the row's log-sum-exp ln(l) + scale * m = (log2(l) + c * m) * ln 2.
-#pragma unroll
-  for (int u = 0; u < SUB; ++u) {
-    const float l = half_sum(lsum[u]);
-    const float inv = 1.f / l;
-    if (args.lse && hf == 0)
-      args.lse[row0 + u * 32 + l32] = (__builtin_amdgcn_logf(l) + m[u] * c) * LN2;
-    _Float16* orow = row_at(o, args.os, b, h, rw0 + u * 32 + l32);
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        h4 out;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float x;
-          if constexpr (ACC16) x = (float)acc16[u][dt][(4 * g + e) >> 1][e & 1];
-          else x = acc[u][dt][4 * g + e];
-          out[e] = (_Float16)(x * inv);
-        }
-        *reinterpret_cast<h4*>(orow + dt * 32 + 8 * g + 4 * hf) = out;
-      }
-    }
-  }
-}
-
 // Workgroup barrier that also drains this wave's outstanding LDS operations,
 // so LDS writes issued before it are visible to every wave after it. The
 // memory clobber keeps the compiler from moving memory accesses across it,
@@ -427,6 +203,28 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
+}
+
+// Trace mode: thread 0 writes the workgroup's record (layout at TRACE_WORDS)
+// with the entry stamps real0/clk0 and stamps taken now.
+__device__ __forceinline__ void trace_record(const FaArgs& args, uint64_t real0, uint64_t clk0,
+                                             int nblk, int bn) {
+  const uint64_t real1 = __builtin_amdgcn_s_memrealtime();
+  const uint64_t clk1 = __builtin_amdgcn_s_memtime();
+  if (threadIdx.x != 0) return;
+  // s_getreg encodings (id | offset << 6 | (size - 1) << 11): HW_ID (id 4)
+  // and XCC_ID (id 20), all 32 bits.
+  const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+  const uint32_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20) & 15u;
+  uint64_t* rec = args.trace + (size_t)blockIdx.x * TRACE_WORDS;
+  rec[0] = (uint64_t)hw | ((uint64_t)xcc << 32);
+  rec[1] = real0;
+  rec[2] = real1;
+  rec[3] = clk0;
+  rec[4] = clk1;
+  rec[5] = blockIdx.x;
+  rec[6] = (uint64_t)nblk;
+  rec[7] = (uint64_t)bn;
 }
 
 // Ping-pong attention body: 8 waves x 32 query rows (BM = 256), two wave
@@ -451,8 +249,15 @@ __device__ __forceinline__ void lds_barrier() {
 // until a block exceeds it by more than TAU, so P <= 2^TAU and the O/l
 // rescale runs only on the rare blocks where some row of the wave needs it.
 // With TAU = 0 the max tracks every increase (FP16 O must not grow).
-template <bool ACC16, int BN, int NS, bool SPLIT_HI, bool CAPTURE>
+template <bool ACC16, int BN, int NS, int MODE>
 __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
+  constexpr bool CAPTURE = MODE == MODE_CAPTURE;
+  constexpr bool TRACE = MODE == MODE_TRACE;
+  uint64_t real0 = 0, clk0 = 0;
+  if constexpr (TRACE) {
+    real0 = __builtin_amdgcn_s_memrealtime();
+    clk0 = __builtin_amdgcn_s_memtime();
+  }
   const _Float16* __restrict__ q = args.q;
   const _Float16* __restrict__ k = args.k;
   const _Float16* __restrict__ vt = args.vt;
@@ -494,9 +299,8 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   const int l32 = lane & 31, hf = lane >> 5;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);   // provably wave-uniform
   // Role: which phase parity this wave's MFMA steps fall on. Waves w and w+4
-  // share a SIMD under round-robin wave placement (SPLIT_HI), waves 2s and
-  // 2s+1 under paired placement.
-  const int grp = SPLIT_HI ? (wave_u >> 2) : (wave_u & 1);
+  // share a SIMD (round-robin wave placement, read back from HW_ID).
+  const int grp = wave_u >> 2;
 
   // Query tiles may run past Nq (a ragged last tile): its rows past the end
   // compute on a copy of the last row and store nothing. Without a mask,
@@ -552,6 +356,7 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
         }
       }
     }
+    if constexpr (TRACE) trace_record(args, real0, clk0, 0, BN);
     if (!row_ok) return;
     if (args.lse && hf == 0) args.lse[grow] = -INFINITY;
     const h4 zero = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
@@ -571,7 +376,7 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   // Group-0 wave dw issues DMA instructions q = dw + 4m (m < NIW, q < NI);
   // q < KI is K instruction q, otherwise V^T instruction q - KI. The per-lane
   // source offset inside a block is fixed, so it is computed once.
-  const int dw = SPLIT_HI ? (wave_u & 3) : (wave_u >> 1);
+  const int dw = wave_u & 3;
   int dma_off[NIW];
 #pragma unroll
   for (int m = 0; m < NIW; ++m) {
@@ -890,6 +695,7 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   }
   // No DMA may still be writing this workgroup's LDS when it exits.
   wait_dma(0);
+  if constexpr (TRACE) trace_record(args, real0, clk0, nblk, BN);
 
   if constexpr (CAPTURE) {
     // Key blocks past the causal diagonal leave every statistic unchanged.
@@ -946,33 +752,23 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
 // LDS bytes the ping-pong body needs for BN-key blocks (a ring of NS K and
 // NS V^T blocks with padded rows).
 constexpr int pp_lds_bytes(int bn, int ns) { return ns * (bn * (HD * 2 + 16) + HD * (bn * 2 + 16)); }
-// Kernel shapes. KIND 0: plain body, P1 = waves per workgroup, P2 = 32-row
-// subtiles per wave. KIND 1: ping-pong body (8 waves x 32 rows), P1 = depth
-// of the LDS ring, P2 = 1 for the w / w+4 wave-role split.
-template <int KIND, int P1>
-constexpr int kThreads = KIND ? 512 : P1 * 64;
-
-template <bool ACC16, int KIND, int P1, int P2, int BN, bool CAP>
-__device__ __forceinline__ void fa_dispatch(const FaArgs& args) {
-  if constexpr (KIND == 0) fa_fwd_body<ACC16, P1, P2, BN>(args);
-  else fa_pp_body<ACC16, BN, P1, P2 == 1, CAP>(args);
-}
 
 // Device entry points, one per accumulation variant. Their names contain the
-// registry names of the backends that launch them, which is how the profiler
-// attributes kernel time (WPE = waves per SIMD the register budget targets).
-// CAP builds the capture-mode variant, a separate kernel so the production
-// kernels carry none of its code.
-template <int KIND, int P1, int P2, int BN, int WPE, bool CAP>
-__global__ void __launch_bounds__((kThreads<KIND, P1>)) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+// backend names of the two accumulation variants, which is how a profile
+// attributes kernel time to a backend. Template parameters: BN keys per
+// block, NS slots in the LDS ring, MODE (production, capture or trace; each
+// mode is a separate kernel, so the production kernels carry none of the
+// debug code). 8 waves of 64 lanes, two per SIMD.
+template <int BN, int NS, int MODE>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 hip_fa_fp32acc_kernel(FaArgs args) {
-  fa_dispatch<false, KIND, P1, P2, BN, CAP>(args);
+  fa_pp_body<false, BN, NS, MODE>(args);
 }
 
-template <int KIND, int P1, int P2, int BN, int WPE, bool CAP>
-__global__ void __launch_bounds__((kThreads<KIND, P1>)) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+template <int BN, int NS, int MODE>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 hip_fa_fp16acc_kernel(FaArgs args) {
-  fa_dispatch<true, KIND, P1, P2, BN, CAP>(args);
+  fa_pp_body<true, BN, NS, MODE>(args);
 }
 
 // ----------------------------------------------------------------------------
@@ -982,63 +778,40 @@ typedef void (*attn_fn)(FaArgs);
 
 struct TileConfig {
   const char* name;
-  int threads;
-  int rows;        // BM
   int keys;        // BN
   int lds;         // dynamic LDS bytes per workgroup
-  bool tails;      // masks ragged query and key tails (any Nq, Nk) and causal masks; has capture mode
-  attn_fn fp32;
-  attn_fn fp16;
-  attn_fn fp32_capture;   // null when the tile has no capture mode
-  attn_fn fp16_capture;
+  attn_fn fn[2][3];   // [acc][mode]
 };
+constexpr int kThreads = 512;     // 8 waves
+constexpr int kRows = 256;        // BM: 8 waves x 32 query rows
 
-#define FA_TILE(NAME, KIND, P1, P2, BN, WPE)                                                 \
-  TileConfig {                                                                             \
-    NAME, kThreads<KIND, P1>, (KIND ? 8 : P1 * P2) * 32, BN,                               \
-        (KIND ? pp_lds_bytes(BN, P1) : 0), KIND == 1,                                      \
-        &hip_fa_fp32acc_kernel<KIND, P1, P2, BN, WPE, false>,                              \
-        &hip_fa_fp16acc_kernel<KIND, P1, P2, BN, WPE, false>,                              \
-        KIND == 1 ? &hip_fa_fp32acc_kernel<KIND, P1, P2, BN, WPE, true> : nullptr,         \
-        KIND == 1 ? &hip_fa_fp16acc_kernel<KIND, P1, P2, BN, WPE, true> : nullptr          \
+#define FA_TILE(NAME, BN, NS)                                                               \
+  TileConfig {                                                                              \
+    NAME, BN, pp_lds_bytes(BN, NS), {                                                       \
+      {&hip_fa_fp32acc_kernel<BN, NS, MODE_RUN>, &hip_fa_fp32acc_kernel<BN, NS, MODE_CAPTURE>, \
+       &hip_fa_fp32acc_kernel<BN, NS, MODE_TRACE>},                                         \
+      {&hip_fa_fp16acc_kernel<BN, NS, MODE_RUN>, &hip_fa_fp16acc_kernel<BN, NS, MODE_CAPTURE>, \
+       &hip_fa_fp16acc_kernel<BN, NS, MODE_TRACE>}                                          \
+    }                                                                                       \
   }
 
+// Every tile masks ragged query and key tails, applies causal masks and has
+// the capture and trace modes.
 const TileConfig kTiles[] = {
-    FA_TILE("w4_r64_n64", 0, 4, 2, 64, 1),     // 4 waves x 64 rows, one wave per SIMD
-    FA_TILE("w8_r32_n64", 0, 8, 1, 64, 2),     // 8 waves x 32 rows, two waves per SIMD
-    FA_TILE("pp_n64_r3", 1, 3, 1, 64, 2),      // ping-pong, 64-key blocks, 3-slot LDS ring
-    FA_TILE("pp_n64_r4", 1, 4, 1, 64, 2),      // ping-pong, 64-key blocks, 4-slot LDS ring
-    FA_TILE("pp_n128_r2", 1, 2, 1, 128, 2),    // ping-pong, 128-key blocks, 2-slot LDS ring
+    FA_TILE("pp_n64_r3", 64, 3),      // 64-key blocks, 3-slot LDS ring
+    FA_TILE("pp_n64_r4", 64, 4),      // 64-key blocks, 4-slot LDS ring
+    FA_TILE("pp_n128_r2", 128, 2),    // 128-key blocks, 2-slot LDS ring
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
-// Automatic choice (fa_problem.kernel == 0): the first of these 1-based tile
-// indices, fastest first (measured at N = 32768 and 65536), that fits the
-// problem (masks tails, or its query-row and key granularity divide Nq and
-// Nk). The FP16 accumulator's 128-key tile spills registers, so that variant
-// prefers a 64-key ring.
-constexpr int kAutoOrderFp32[] = {5, 4, 3, 2, 1};
-constexpr int kAutoOrderFp16[] = {3, 4, 5, 2, 1};
-static_assert(sizeof(kAutoOrderFp32) == sizeof(int) * kNumTiles &&
-                  sizeof(kAutoOrderFp16) == sizeof(int) * kNumTiles,
-              "every tile appears in each automatic order");
-
-bool tile_fits(const TileConfig& t, const fa_problem* p) {
-  if (p->causal != FA_CAUSAL_NONE) return t.tails;
-  return t.tails || (p->seq_q > 0 && p->seq_k > 0 && p->seq_q % t.rows == 0 && p->seq_k % t.keys == 0);
-}
+// Automatic choice (fa_problem.kernel == 0), measured fastest at N = 32768
+// and 65536: the 128-key tile for FP32 O; for FP16 O, whose 128-key tile
+// spills registers, the 3-slot 64-key ring.
+constexpr int kAutoFp32 = 3;
+constexpr int kAutoFp16 = 1;
 
 int select_tile(const fa_problem* p, const TileConfig** out) {
   int idx = p->kernel;
-  if (idx == 0) {
-    const int* order = p->acc == FA_ACC_FP16 ? kAutoOrderFp16 : kAutoOrderFp32;
-    idx = order[0];
-    for (int n = 0; n < kNumTiles; ++n) {
-      if (tile_fits(kTiles[order[n] - 1], p)) {
-        idx = order[n];
-        break;
-      }
-    }
-  }
+  if (idx == 0) idx = p->acc == FA_ACC_FP16 ? kAutoFp16 : kAutoFp32;
   if (idx < 1 || idx > kNumTiles) return FA_ERR_KERNEL;
   *out = &kTiles[idx - 1];
   return FA_OK;
@@ -1079,15 +852,13 @@ int validate(const fa_problem* p, const TileConfig** tile) {
     return FA_ERR_CAUSAL;
   int rc = select_tile(p, tile);
   if (rc) return rc;
-  if (p->causal != FA_CAUSAL_NONE && !(*tile)->tails) return FA_ERR_CAUSAL;
   // 32-bit index limits used inside the kernels (the padded key length too).
   const int64_t lim = (int64_t)1 << 30;
   if (p->seq_q >= lim || p->seq_k >= lim - 128 || p->heads_q >= lim || p->batch >= lim)
     return FA_ERR_GEOMETRY;
   const int64_t bh = p->batch * p->heads_q;
-  const int64_t tiles_q = (p->seq_q + (*tile)->rows - 1) / (*tile)->rows;
+  const int64_t tiles_q = (p->seq_q + kRows - 1) / kRows;
   if (bh >= lim || bh * tiles_q >= lim || p->batch * p->heads_kv >= 65536) return FA_ERR_GEOMETRY;
-  if (!tile_fits(**tile, p)) return FA_ERR_TAIL;
   // The kernels address a V^T row (Nk' keys) with 32-bit byte offsets.
   if ((int64_t)HD * 2 * key_layout(p, *tile).nk_pad >= ((int64_t)1 << 31)) return FA_ERR_GEOMETRY;
   return FA_OK;
@@ -1096,6 +867,11 @@ int validate(const fa_problem* p, const TileConfig** tile) {
 // FP32 values capture mode writes: 4 statistics x key blocks x B * Hq * Nq rows.
 uint64_t capture_count(const fa_problem* p, const TileConfig* tile, const KeyLayout& lay) {
   return 4ull * (uint64_t)(lay.nk_pad / tile->keys) * (uint64_t)(p->batch * p->heads_q * p->seq_q);
+}
+
+// Workgroups of one attention launch (one per 256 query rows of a (b, h)).
+uint64_t grid_size(const fa_problem* p) {
+  return (uint64_t)(p->batch * p->heads_q) * (uint64_t)((p->seq_q + kRows - 1) / kRows);
 }
 
 // Strides of a contiguous [B, H, N, 128] tensor.
@@ -1118,9 +894,37 @@ int check_strides(const fa_problem* p, const fa_strides* s, const KeyLayout& lay
   return FA_OK;
 }
 
+// Tiles above 64 KiB of LDS need the per-kernel dynamic-LDS limit raised,
+// once per kernel function and device. The flags are the library's only
+// state; setting one twice (two threads racing on a first call) is harmless.
+constexpr int kMaxDevices = 64;
+std::atomic<uint8_t> g_lds_ready[kMaxDevices][kNumTiles][2][3];
+
+int ensure_lds_limit(const TileConfig* tile, int acc, int mode) {
+  if (tile->lds <= 65536) return FA_OK;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FA_ERR_LAUNCH;
+  std::atomic<uint8_t>& ready = g_lds_ready[dev][tile - kTiles][acc][mode];
+  if (ready.load(std::memory_order_acquire)) return FA_OK;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(tile->fn[acc][mode]),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, tile->lds) != hipSuccess)
+    return FA_ERR_LAUNCH;
+  ready.store(1, std::memory_order_release);
+  return FA_OK;
+}
+
+// Optional outputs of one launch: per-row LSE, capture statistics, trace records.
+struct Extras {
+  float* lse = nullptr;
+  float* stats = nullptr;
+  uint64_t stats_count = 0;
+  uint64_t* trace = nullptr;
+  uint64_t trace_count = 0;
+};
+
 int launch(const fa_problem* p, const fa_strides* strides, const void* q, const void* k,
-           const void* v, void* o, float* lse, float* stats, uint64_t stats_count,
-           void* workspace, uint64_t workspace_bytes, void* stream) {
+           const void* v, void* o, const Extras& ex, void* workspace, uint64_t workspace_bytes,
+           void* stream) {
   const TileConfig* tile = nullptr;
   int rc = validate(p, &tile);
   if (rc) return rc;
@@ -1137,30 +941,41 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
     os = strides_of(strides->o);
   }
   if (!workspace || workspace_bytes < lay.vt_bytes + lay.k_bytes) return FA_ERR_WORKSPACE;
-  for (const void* ptr : {q, k, v, (const void*)o, (const void*)workspace, (const void*)lse,
-                          (const void*)stats})
+  for (const void* ptr : {q, k, v, (const void*)o, (const void*)workspace, (const void*)ex.lse,
+                          (const void*)ex.stats, (const void*)ex.trace})
     if (reinterpret_cast<uintptr_t>(ptr) & 15) return FA_ERR_ALIGN;
-  if (stats && (!tile->fp32_capture || stats_count < capture_count(p, tile, lay)))
-    return FA_ERR_CAPTURE;
+  if (ex.stats && ex.stats_count < capture_count(p, tile, lay)) return FA_ERR_CAPTURE;
+  if (ex.trace && ex.trace_count < grid_size(p) * TRACE_WORDS) return FA_ERR_TRACE;
+  const int acc = p->acc == FA_ACC_FP16 ? 1 : 0;
+  const int mode = ex.stats ? MODE_CAPTURE : ex.trace ? MODE_TRACE : MODE_RUN;
+  rc = ensure_lds_limit(tile, acc, mode);
+  if (rc) return rc;
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   _Float16* vt = static_cast<_Float16*>(workspace);
   _Float16* kpad = lay.pad_k ? vt + lay.vt_bytes / sizeof(_Float16) : nullptr;
 
-  (void)hipGetLastError();  // clear any stale error so the checks below see only ours
-  dim3 prep_grid((unsigned)(lay.nk_pad / VT_GROUP), (unsigned)(p->batch * p->heads_kv));
-  hipLaunchKernelGGL(fa_prep_kernel, prep_grid, dim3(256), 0, st, static_cast<const _Float16*>(k),
-                     static_cast<const _Float16*>(v), vt, kpad, (int)p->seq_k, (int)lay.nk_pad,
-                     (int)p->heads_kv, ks, vs);
-  if (hipGetLastError() != hipSuccess) return FA_ERR_LAUNCH;
+  // hipLaunchKernel returns the status of this launch alone; errors left
+  // pending by the caller's earlier work are neither read nor cleared.
+  {
+    const _Float16* kk = static_cast<const _Float16*>(k);
+    const _Float16* vv = static_cast<const _Float16*>(v);
+    int nk_valid = (int)p->seq_k, nk_pad = (int)lay.nk_pad, heads_kv = (int)p->heads_kv;
+    void* prep_args[] = {&kk, &vv, &vt, &kpad, &nk_valid, &nk_pad, &heads_kv, &ks, &vs};
+    const dim3 prep_grid((unsigned)(lay.nk_pad / VT_GROUP), (unsigned)(p->batch * p->heads_kv));
+    if (hipLaunchKernel(reinterpret_cast<const void*>(&fa_prep_kernel), prep_grid, dim3(256),
+                        prep_args, 0, st) != hipSuccess)
+      return FA_ERR_LAUNCH;
+  }
 
   FaArgs args;
   args.q = static_cast<const _Float16*>(q);
   args.k = lay.pad_k ? kpad : static_cast<const _Float16*>(k);
   args.vt = vt;
   args.o = static_cast<_Float16*>(o);
-  args.lse = lse;
-  args.stats = stats;
+  args.lse = ex.lse;
+  args.stats = ex.stats;
+  args.trace = ex.trace;
   args.heads_q = (int)p->heads_q;
   args.group = (int)(p->heads_q / p->heads_kv);
   args.seq_q = (int)p->seq_q;
@@ -1172,16 +987,11 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
   args.qs = qs;
   args.os = os;
   args.ks = lay.pad_k ? contiguous(p->heads_kv, lay.nk_pad) : ks;
-  const int64_t tiles_q = (p->seq_q + tile->rows - 1) / tile->rows;
-  const unsigned grid = (unsigned)(p->batch * p->heads_q * tiles_q);
-  attn_fn fn = stats ? (p->acc == FA_ACC_FP16 ? tile->fp16_capture : tile->fp32_capture)
-                     : (p->acc == FA_ACC_FP16 ? tile->fp16 : tile->fp32);
-  if (tile->lds > 65536 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, tile->lds) != hipSuccess)
+  void* attn_args[] = {&args};
+  if (hipLaunchKernel(reinterpret_cast<const void*>(tile->fn[acc][mode]),
+                      dim3((unsigned)grid_size(p)), dim3(kThreads), attn_args, tile->lds,
+                      st) != hipSuccess)
     return FA_ERR_LAUNCH;
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(tile->threads), tile->lds, st, args);
-  if (hipGetLastError() != hipSuccess) return FA_ERR_LAUNCH;
   return FA_OK;
 }
 
@@ -1204,8 +1014,8 @@ int fa_fwd_tile(const fa_problem* p, int32_t* rows, int32_t* keys) {
   const TileConfig* tile = nullptr;
   int rc = select_tile(p, &tile);
   if (rc) return rc;
-  *rows = tile->tails ? 1 : tile->rows;
-  *keys = tile->tails ? 1 : tile->keys;
+  *rows = 1;          // every tile masks ragged query and key tails
+  *keys = 1;
   return FA_OK;
 }
 
@@ -1220,19 +1030,23 @@ int fa_fwd_select(const fa_problem* p, int32_t* kernel) {
 
 int fa_fwd(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
            void* workspace, uint64_t workspace_bytes, void* stream) {
-  return launch(p, nullptr, q, k, v, o, nullptr, nullptr, 0, workspace, workspace_bytes, stream);
+  return launch(p, nullptr, q, k, v, o, Extras{}, workspace, workspace_bytes, stream);
 }
 
 int fa_fwd_lse(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
                float* lse, void* workspace, uint64_t workspace_bytes, void* stream) {
-  return launch(p, nullptr, q, k, v, o, lse, nullptr, 0, workspace, workspace_bytes, stream);
+  Extras ex;
+  ex.lse = lse;
+  return launch(p, nullptr, q, k, v, o, ex, workspace, workspace_bytes, stream);
 }
 
 int fa_fwd_strided(const fa_problem* p, const fa_strides* strides, const void* q, const void* k,
                    const void* v, void* o, float* lse, void* workspace, uint64_t workspace_bytes,
                    void* stream) {
   if (!strides) return FA_ERR_NULL;
-  return launch(p, strides, q, k, v, o, lse, nullptr, 0, workspace, workspace_bytes, stream);
+  Extras ex;
+  ex.lse = lse;
+  return launch(p, strides, q, k, v, o, ex, workspace, workspace_bytes, stream);
 }
 
 int fa_fwd_capture_count(const fa_problem* p, uint64_t* count, int32_t* block_keys) {
@@ -1240,7 +1054,6 @@ int fa_fwd_capture_count(const fa_problem* p, uint64_t* count, int32_t* block_ke
   const TileConfig* tile = nullptr;
   int rc = validate(p, &tile);
   if (rc) return rc;
-  if (!tile->fp32_capture) return FA_ERR_CAPTURE;
   *count = capture_count(p, tile, key_layout(p, tile));
   *block_keys = tile->keys;
   return FA_OK;
@@ -1250,7 +1063,30 @@ int fa_fwd_capture(const fa_problem* p, const void* q, const void* k, const void
                    float* lse, float* stats, uint64_t stats_count, void* workspace,
                    uint64_t workspace_bytes, void* stream) {
   if (!stats) return FA_ERR_NULL;
-  return launch(p, nullptr, q, k, v, o, lse, stats, stats_count, workspace, workspace_bytes, stream);
+  Extras ex;
+  ex.lse = lse;
+  ex.stats = stats;
+  ex.stats_count = stats_count;
+  return launch(p, nullptr, q, k, v, o, ex, workspace, workspace_bytes, stream);
+}
+
+int fa_fwd_trace_count(const fa_problem* p, uint64_t* count) {
+  if (!count) return FA_ERR_NULL;
+  const TileConfig* tile = nullptr;
+  int rc = validate(p, &tile);
+  if (rc) return rc;
+  *count = grid_size(p) * TRACE_WORDS;
+  return FA_OK;
+}
+
+int fa_fwd_trace(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
+                 uint64_t* trace, uint64_t trace_count, void* workspace, uint64_t workspace_bytes,
+                 void* stream) {
+  if (!trace) return FA_ERR_NULL;
+  Extras ex;
+  ex.trace = trace;
+  ex.trace_count = trace_count;
+  return launch(p, nullptr, q, k, v, o, ex, workspace, workspace_bytes, stream);
 }
 
 int fa_kernel_count(void) { return kNumTiles; }
@@ -1266,15 +1102,16 @@ const char* fa_strerror(int status) {
     case FA_ERR_NULL: return "required pointer is NULL";
     case FA_ERR_GEOMETRY: return "invalid attention geometry";
     case FA_ERR_DIM: return "head dimension must be 128";
-    case FA_ERR_TAIL: return "unsupported query/key tail: Nq or Nk not a multiple of the selected tile, which has no masked tail";
+    case FA_ERR_TAIL: return "unsupported query/key tail (no longer returned: every tile masks tails)";
     case FA_ERR_ALIGN: return "tensor pointer not 16-byte aligned";
     case FA_ERR_WORKSPACE: return "workspace missing or too small";
     case FA_ERR_ACC: return "unknown accumulation variant";
     case FA_ERR_SCALE: return "scale must be finite and positive";
     case FA_ERR_KERNEL: return "unknown kernel selector";
     case FA_ERR_LAUNCH: return "HIP kernel launch failed";
-    case FA_ERR_CAPTURE: return "capture needs a ping-pong tile and a stats buffer of fa_fwd_capture_count() floats";
-    case FA_ERR_CAUSAL: return "unknown causal mode, or a causal mask asked of a tile without masking";
+    case FA_ERR_CAPTURE: return "capture needs a stats buffer of fa_fwd_capture_count() floats";
+    case FA_ERR_CAUSAL: return "unknown causal mode";
+    case FA_ERR_TRACE: return "trace needs a buffer of fa_fwd_trace_count() 64-bit words";
     default: return "unknown status";
   }
 }

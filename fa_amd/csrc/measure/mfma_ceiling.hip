@@ -1,0 +1,128 @@
+// Sustained dense FP16 MFMA rate of the board: a measurement kernel, not part
+// of the attention library. It shares the attention kernel's launch shape
+// (8 waves of 64 lanes per workgroup, two waves per SIMD, one workgroup per
+// CU at a time) and its matrix instruction (v_mfma_f32_32x32x16_f16), and
+// does nothing but issue those instructions for a fixed number of
+// iterations, so its rate is what the matrix cores sustain on this board
+// under its power limit when nothing else runs beside them.
+//
+//   MODE 0  operands in registers: the matrix pipe alone.
+//   MODE 1  each MFMA's A operand is first read from LDS (one ds_read_b128
+//           per lane, four reads in flight), as a GEMM or the attention
+//           kernel's MFMA step feeds the pipe.
+//
+// Operands are FP16 values supplied by the caller (random normal data, so the
+// datapath toggles as it does on real inputs). Every wave keeps four
+// independent accumulators (a dependent MFMA reuses its accumulator four
+// instructions later) and writes their sum at the end, so no MFMA is dead.
+// With a trace buffer, thread 0 of every workgroup records s_memrealtime and
+// s_memtime at entry and after the loop (words 1-4 of an 8-word record, the
+// attention kernel's trace layout), from which the running shader clock
+// follows.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 512;
+constexpr int kOperandHalves = 8192;   // 16 KiB of FP16 operands
+constexpr int kTraceWords = 8;
+constexpr int kMfmaPerIter = 16;
+
+__device__ __forceinline__ f32x16 mfma32(h8 a, h8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+template <int MODE>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+fa_mfma_ceiling_kernel(const _Float16* __restrict__ operands, float* __restrict__ out,
+                       uint64_t* __restrict__ trace, int iters) {
+  const uint64_t real0 = __builtin_amdgcn_s_memrealtime();
+  const uint64_t clk0 = __builtin_amdgcn_s_memtime();
+  __shared__ __attribute__((aligned(16))) _Float16 lds[kOperandHalves];
+  const int tid = threadIdx.x, lane = tid & 63;
+  for (int i = tid; i < kOperandHalves / 8; i += kThreads)
+    reinterpret_cast<h8*>(lds)[i] = reinterpret_cast<const h8*>(operands)[i];
+  h8 a[4], b[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    a[j] = reinterpret_cast<const h8*>(operands)[(j * 64 + lane) & (kOperandHalves / 8 - 1)];
+    b[j] = reinterpret_cast<const h8*>(operands)[(256 + j * 64 + lane) & (kOperandHalves / 8 - 1)];
+  }
+  __syncthreads();
+  f32x16 acc[4] = {};
+  // LDS operand address of MFMA n of an iteration: 16 B per lane, 1 KiB per
+  // MFMA, cycling through the 16 KiB buffer (distinct lanes, distinct banks).
+  const char* base = reinterpret_cast<const char*>(lds) + lane * 16;
+  for (int it = 0; it < iters; ++it) {
+    if constexpr (MODE == 0) {
+#pragma unroll
+      for (int n = 0; n < kMfmaPerIter; ++n) acc[n & 3] = mfma32(a[n >> 2], b[n & 3], acc[n & 3]);
+    } else {
+      h8 fr[4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) fr[n] = *reinterpret_cast<const h8*>(base + n * 1024);
+#pragma unroll
+      for (int n = 0; n < kMfmaPerIter; ++n) {
+        const h8 x = fr[n & 3];
+        if (n + 4 < kMfmaPerIter) fr[n & 3] = *reinterpret_cast<const h8*>(base + (n + 4) * 1024);
+        acc[n & 3] = mfma32(x, b[n & 3], acc[n & 3]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sum += acc[j][r];
+  out[(size_t)blockIdx.x * kThreads + tid] = sum;
+  if (trace) {
+    const uint64_t real1 = __builtin_amdgcn_s_memrealtime();
+    const uint64_t clk1 = __builtin_amdgcn_s_memtime();
+    if (tid == 0) {
+      uint64_t* rec = trace + (size_t)blockIdx.x * kTraceWords;
+      rec[0] = 0;
+      rec[1] = real0;
+      rec[2] = real1;
+      rec[3] = clk0;
+      rec[4] = clk1;
+      rec[5] = blockIdx.x;
+      rec[6] = (uint64_t)iters;
+      rec[7] = kMfmaPerIter;
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+// FP16 FLOPs one workgroup performs: 8 waves x iters x 16 MFMAs x 32x32x16x2.
+uint64_t fa_ceiling_flops_per_workgroup(int iters) {
+  return (uint64_t)(kThreads / 64) * (uint64_t)iters * kMfmaPerIter * 32 * 32 * 16 * 2;
+}
+
+// Launch the ceiling kernel: mode 0 (register operands) or 1 (LDS-fed A
+// operand); operands = 8192 FP16 values (16-byte aligned), out = workgroups
+// x 512 floats, trace = workgroups x 8 words or NULL. Returns 0, or 1 for
+// bad arguments, 2 when the launch is rejected.
+int fa_ceiling_mfma(int mode, int workgroups, int iters, const void* operands, float* out,
+                    uint64_t* trace, void* stream) {
+  if (mode < 0 || mode > 1 || workgroups <= 0 || iters <= 0 || !operands || !out) return 1;
+  if ((reinterpret_cast<uintptr_t>(operands) | reinterpret_cast<uintptr_t>(out) |
+       reinterpret_cast<uintptr_t>(trace)) & 15)
+    return 1;
+  const _Float16* ops = static_cast<const _Float16*>(operands);
+  void* args[] = {&ops, &out, &trace, &iters};
+  const void* fn = mode == 0 ? reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<0>)
+                             : reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<1>);
+  return hipLaunchKernel(fn, dim3((unsigned)workgroups), dim3(kThreads), args, 0,
+                         static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : 2;
+}
+
+}  // extern "C"

@@ -1,0 +1,152 @@
+"""The board's sustained dense FP16 matrix rate, the ceiling the attention kernel runs under.
+
+Two measurements, both on the GPU, both timed with HIP events on torch's
+current stream after warmup launches:
+
+* ``mfma_loop`` -- ``libfa_ceiling.so``: every SIMD of every CU issuing
+  nothing but ``v_mfma_f32_32x32x16_f16`` (the attention kernel's matrix
+  instruction) from two waves, in the attention kernel's launch shape, with
+  random FP16 operands either in registers (mode 0) or with each A operand
+  read from LDS first (mode 1). Its trace records give the clock it ran at.
+* ``gemm`` -- torch's FP16 matrix product (hipBLASLt) on large square and
+  rectangular shapes, the rate a tuned vendor GEMM reaches.
+
+The MI355X's nominal dense FP16 peak, 2516.6 TFLOP/s, assumes every CU at
+2.4 GHz; under sustained matrix load the board lowers its clock to stay within
+its power limit, so these rates (and the clock the loop reports) are the
+practical ceiling an MFMA-bound kernel is measured against.
+
+``python -m fa_amd.measure.ceiling [--out FILE]`` prints (and writes) the
+summary; ``measure()`` returns it as a dict for bench.py.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import os
+import sys
+
+GEMM_SHAPES = ((8192, 8192, 8192), (8192, 8192, 16384), (16384, 16384, 8192))
+
+
+def _library():
+    from fa_amd import build
+
+    lib = C.CDLL(str(build.CEILING.library), mode=C.RTLD_LOCAL)
+    lib.fa_ceiling_flops_per_workgroup.restype = C.c_uint64
+    lib.fa_ceiling_flops_per_workgroup.argtypes = [C.c_int]
+    lib.fa_ceiling_mfma.restype = C.c_int
+    lib.fa_ceiling_mfma.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
+                                    C.c_void_p, C.c_void_p]
+    return lib
+
+
+def mfma_loop(mode, workgroups=2048, iters=16384, reps=3, warmup=2):
+    """(TFLOP/s, trace records) of the MFMA-only kernel in ``mode``."""
+    import torch
+
+    lib = _library()
+    g = torch.Generator().manual_seed(7)
+    operands = torch.randn(8192, generator=g).half().cuda()
+    out = torch.empty(workgroups * 512, dtype=torch.float32, device="cuda")
+    trace = torch.zeros(workgroups, 8, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def launch(with_trace):
+        rc = lib.fa_ceiling_mfma(mode, workgroups, iters, operands.data_ptr(), out.data_ptr(),
+                                 trace.data_ptr() if with_trace else None,
+                                 C.c_void_p(stream.cuda_stream))
+        if rc:
+            raise RuntimeError(f"fa_ceiling_mfma failed with status {rc}")
+
+    for _ in range(warmup):
+        launch(False)
+    torch.cuda.synchronize()
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    begin.record(stream)
+    for _ in range(reps):
+        launch(False)
+    end.record(stream)
+    torch.cuda.synchronize()
+    seconds = begin.elapsed_time(end) / 1e3 / reps
+    launch(True)
+    torch.cuda.synchronize()
+    if not torch.isfinite(out).all():
+        raise RuntimeError("MFMA ceiling kernel produced non-finite sums")
+    flops = lib.fa_ceiling_flops_per_workgroup(iters) * workgroups
+    return flops / seconds / 1e12, trace.cpu().numpy()
+
+
+def gemm(shapes=GEMM_SHAPES, reps=20, warmup=3):
+    """{(m, n, k): TFLOP/s} of torch FP16 matmul (A [m,k] @ B [k,n], N(0,1) data)."""
+    import torch
+
+    rates = {}
+    g = torch.Generator().manual_seed(11)
+    for m, n, k in shapes:
+        a = torch.randn(m, k, generator=g).half().cuda()
+        b = torch.randn(k, n, generator=g).half().cuda()
+        for _ in range(warmup):
+            a @ b
+        torch.cuda.synchronize()
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record()
+        for _ in range(reps):
+            a @ b
+        end.record()
+        torch.cuda.synchronize()
+        rates[(m, n, k)] = 2.0 * m * n * k * reps / (begin.elapsed_time(end) / 1e3) / 1e12
+        del a, b
+    return rates
+
+
+def measure(gemm_reps=20, loop_iters=16384):
+    from fa_amd.measure import clock
+
+    out = {"gemm_tflops": {}, "mfma_loop": {}}
+    for shape, rate in gemm(reps=gemm_reps).items():
+        out["gemm_tflops"]["x".join(map(str, shape))] = round(rate, 1)
+    for mode, label in ((0, "registers"), (1, "lds_operand")):
+        rate, records = mfma_loop(mode, iters=loop_iters)
+        s = clock.summarize(records)
+        out["mfma_loop"][label] = {"tflops": round(rate, 1),
+                                   "clock_mhz": round(s["mean_mhz_time_weighted"], 0)}
+    out["gemm_best_tflops"] = max(out["gemm_tflops"].values())
+    out["mfma_loop_best_tflops"] = max(v["tflops"] for v in out["mfma_loop"].values())
+    return out
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--out")
+    ap.add_argument("--command", default="")
+    args = ap.parse_args(argv)
+    repo = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    if repo not in sys.path:
+        sys.path.insert(0, repo)
+    from fa_amd.measure import clock
+
+    lines = ["# sustained dense FP16 matrix rate of this board (nominal peak 2516.6 TFLOP/s)",
+             f"command: {args.command or 'python -m fa_amd.measure.ceiling ' + ' '.join(argv or sys.argv[1:])}"]
+    for shape, rate in gemm().items():
+        lines.append(f"gemm_fp16 {shape[0]}x{shape[1]}x{shape[2]} (torch.matmul, hipBLASLt): "
+                     f"{rate:.1f} TFLOP/s = {rate / clock.PEAK_TFLOPS:.3f} of nominal")
+        print(lines[-1], flush=True)
+    for mode, label in ((0, "operands in registers"), (1, "A operand read from LDS")):
+        rate, records = mfma_loop(mode)
+        s = clock.summarize(records)
+        f = s["mean_mhz_time_weighted"]
+        lines.append(f"mfma_loop mode {mode} ({label}): {rate:.1f} TFLOP/s = "
+                     f"{rate / clock.PEAK_TFLOPS:.3f} of nominal; clock {f:.0f} MHz "
+                     f"(p10 {s['p10_mhz']:.0f}, p90 {s['p90_mhz']:.0f}); "
+                     f"{rate / clock.roof_at(f):.3f} of the roof at that clock")
+        print(lines[-1], flush=True)
+    if args.out:
+        with open(args.out, "w", encoding="utf-8") as fh:
+            fh.write("\n".join(lines) + "\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

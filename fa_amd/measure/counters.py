@@ -5,13 +5,13 @@ median per-dispatch value of every collected counter (summed over the rows
 rocprofv3 writes per dispatch), so a counter pass can be kept under
 ``profiles/`` as text next to the command that produced it.
 
-Usage: python -m fa_amd.core.counters <rocprofv3 output dir> --match hip_fa_fp32acc
+Usage: python -m fa_amd.measure.counters <rocprofv3 output dir> --match hip_fa_fp32acc
 """
 
 import argparse
 import statistics
 
-from fa_amd.core.traffic import per_dispatch, pick
+from fa_amd.measure.traffic import per_dispatch, pick
 
 
 def summarize(folder, needle, counters):

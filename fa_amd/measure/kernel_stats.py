@@ -6,7 +6,7 @@ view ``kernels`` with ``name`` and ``duration`` in ns) or, for runs made with
 kernel: calls, average/min/max duration in ns and share of the total. The
 text is what ``profiles/`` keeps for a workload.
 
-Usage: python -m fa_amd.core.kernel_stats <rocprofv3 output dir> [--flops F --match NAME]
+Usage: python -m fa_amd.measure.kernel_stats <rocprofv3 output dir> [--flops F --match NAME]
 ``--flops`` adds the achieved TFLOP/s of the kernel whose name contains
 ``--match`` (average duration).
 """

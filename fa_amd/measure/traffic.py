@@ -10,7 +10,7 @@ figures are added: ``traffic_bytes_per_launch``. The summary file this writes
 under ``profiles/`` is what ``bench.py`` reports as ``roofline.traffic``.
 
 Usage (on the CPU, after the GPU runs):
-  python -m fa_amd.core.traffic --fetch DIR --write DIR --copy-mib M \\
+  python -m fa_amd.measure.traffic --fetch DIR --write DIR --copy-mib M \\
       --key "<backend> c<i> <case> tile=<tile>" --command-fetch "..." \\
       --command-write "..." --out profiles/<name>_traffic.txt
 """

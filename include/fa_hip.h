@@ -16,9 +16,11 @@
  * Conventions (mirroring the reference's two-phase operator binding):
  *   - every entry point returns 0 on success and a nonzero FA_ERR_* code
  *     otherwise; fa_strerror() names the code;
- *   - nothing here allocates device memory, aborts, or keeps mutable global
- *     state: the caller owns q, k, v, o and the workspace, and calls on
- *     different streams are independent;
+ *   - nothing here allocates device memory or aborts: the caller owns q, k,
+ *     v, o and the workspace, and calls on different streams with different
+ *     workspaces are independent. The only library state is a per-device,
+ *     per-kernel flag recording that the kernel's dynamic-LDS limit has been
+ *     raised (set on first use);
  *   - fa_fwd() is asynchronous on the given stream (a hipStream_t passed as
  *     void*, NULL for the default stream).
  *
@@ -39,21 +41,29 @@ enum fa_status {
   FA_ERR_NULL = 1,          /* a required pointer is NULL */
   FA_ERR_GEOMETRY = 2,      /* non-positive size, Hq % Hkv != 0, or overflowing sizes */
   FA_ERR_DIM = 3,           /* head dimension other than 128 */
-  FA_ERR_TAIL = 4,          /* Nq or Nk not a multiple of an explicitly selected tile without masked tails */
+  FA_ERR_TAIL = 4,          /* reserved: no longer returned (every tile masks ragged tails) */
   FA_ERR_ALIGN = 5,         /* a tensor pointer is not 16-byte aligned */
   FA_ERR_WORKSPACE = 6,     /* workspace missing or smaller than fa_fwd_workspace_bytes() */
   FA_ERR_ACC = 7,           /* unknown accumulation variant */
   FA_ERR_SCALE = 8,         /* scale not finite and positive */
   FA_ERR_KERNEL = 9,        /* unknown kernel selector */
   FA_ERR_LAUNCH = 10,       /* the HIP runtime rejected a launch */
-  FA_ERR_CAPTURE = 11,      /* capture asked of a tile without it, or stats buffer too small */
-  FA_ERR_CAUSAL = 12        /* unknown causal mode, or a causal mask asked of a tile without masking */
+  FA_ERR_CAPTURE = 11,      /* capture stats buffer too small */
+  FA_ERR_CAUSAL = 12,       /* unknown causal mode */
+  FA_ERR_TRACE = 13         /* trace buffer too small */
 };
 
 enum fa_acc {
   FA_ACC_FP32 = 0,          /* O accumulated in FP32 registers across all keys */
   FA_ACC_FP16 = 1           /* per-block PV rounded to FP16, O accumulated in FP16 */
 };
+/* Range of the FP16 accumulator: O is accumulated unnormalised, as
+ * sum_j 2^(s_j c - m c) v_j over the keys seen so far, with m the running
+ * row max, so every weight is <= 1 but the sum is not. Once that sum leaves
+ * the FP16 range (|.| > 65504, e.g. a long row of nearly equal scores whose
+ * values have a mean of ~1: Nk * |mean v| > 65504) the accumulator becomes
+ * +-inf and the row's output is inf or NaN. The reference's FP16-O kernel has
+ * the same limit (its O is FP16 as well). FA_ACC_FP32 has no such limit. */
 
 /* Attention mask. The reference runs full attention only (sparse_mode=0 in
  * backends/npu_fa/backend.py:48, is_causal=False in
@@ -146,8 +156,7 @@ int fa_fwd_strided(const fa_problem* p, const fa_strides* strides, const void* q
  *   z      the block's own sum of (FP16-rounded) probabilities, relative to m;
  * so m + ln l is the log-sum-exp of every key so far and m + ln z that of
  * the block. fa_fwd_capture_count() gives the float count and the block size
- * (key blocks nblk = ceil(Nk / block_keys)). Ping-pong tiles only (the
- * automatic choice); meant for small debug inputs.
+ * (key blocks nblk = ceil(Nk / block_keys)). Meant for small debug inputs.
  */
 int fa_fwd_capture_count(const fa_problem* p, uint64_t* count, int32_t* block_keys);
 int fa_fwd_capture(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
@@ -155,11 +164,35 @@ int fa_fwd_capture(const fa_problem* p, const void* q, const void* k, const void
                    uint64_t workspace_bytes, void* stream);
 
 /*
- * Query-row and key granularity the kernel fa_fwd() would use for *p needs:
- * Nq must be a multiple of *rows and Nk of *keys (1 and 1 for the tiles that
- * mask ragged tails, which the automatic choice always picks). Host-side
- * counterpart of the reference binding's alignment check (binding.py:95),
- * which demands Nq % 256 == 0 and Nk % 512 == 0.
+ * Trace mode: fa_fwd() that also writes one record of 8 uint64 words per
+ * workgroup of the attention kernel into trace (16-byte aligned, at least
+ * fa_fwd_trace_count() words), the counterpart of the reference kernel's
+ * per-core trace output, which records each core's id and its start and end
+ * system-counter values (K32/panel_kernel.h:222-225,340-342; buffer
+ * binding.py:44). Record of workgroup w, words 8w .. 8w+7:
+ *   0  HW_ID register (bits 0-31) and XCC_ID (bits 32-35) of wave 0
+ *   1  s_memrealtime at entry (100 MHz reference clock)
+ *   2  s_memrealtime after the key loop
+ *   3  s_memtime at entry (shader clock cycles)
+ *   4  s_memtime after the key loop
+ *   5  workgroup index w
+ *   6  key blocks streamed
+ *   7  keys per block
+ * so the shader clock the workgroup ran at is (w4 - w3) / (w2 - w1) * 100
+ * MHz. The trace kernel is a separate instantiation of the same tile (the
+ * production kernels carry no stamps); its O is the production kernel's.
+ */
+int fa_fwd_trace_count(const fa_problem* p, uint64_t* count);
+int fa_fwd_trace(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
+                 uint64_t* trace, uint64_t trace_count, void* workspace, uint64_t workspace_bytes,
+                 void* stream);
+
+/*
+ * Query-row and key granularity fa_fwd() needs for *p: Nq must be a
+ * multiple of *rows and Nk of *keys. Every tile masks ragged query and key
+ * tails, so both are 1 for any valid selector. Host-side counterpart of the
+ * reference binding's alignment check (binding.py:95), which demands
+ * Nq % 256 == 0 and Nk % 512 == 0.
  */
 int fa_fwd_tile(const fa_problem* p, int32_t* rows, int32_t* keys);
 

@@ -320,22 +320,18 @@ def kernel_ids():
 
 def tile_of(kernel):
     """(query rows, keys) of one workgroup block of tile configuration ``kernel``,
-    from its name: w{waves}_r{rows per wave}_n{keys} or pp_n{keys}_r{ring} (256 rows)."""
+    from its name pp_n{keys}_r{ring}: 256 query rows per workgroup."""
     from fa_amd import binding, build
 
     name = binding.load_library(build.LIBRARY).fa_kernel_name(kernel).decode()
     parts = dict((p[0], int(p[1:])) for p in name.split("_")[1:])
-    if name.startswith("pp_"):
-        return 256, parts["n"]
-    return int(name.split("_")[0][1:]) * parts["r"], parts["n"]
+    return 256, parts["n"]
 
 
 @pytest.mark.parametrize("shape", ["long", "one_block", "stress", "ragged"])
 @pytest.mark.parametrize("kernel", kernel_ids())
 def test_every_tile_config(library_path, kernel, shape):
     rows, keys = tile_of(kernel)
-    if shape == "ragged" and not kernel_name(kernel).startswith("pp_"):
-        pytest.skip("plain tiles need whole query and key blocks")
     nq, nk, stress = {"long": (2048, 2048, False), "one_block": (2 * rows, keys, False),
                       "stress": (rows, 3 * keys, True),
                       "ragged": (rows + 37, 2 * keys + 5, True)}[shape]
@@ -434,8 +430,7 @@ def test_causal_vs_f64(library_path, b, hq, hkv, nq, nk, sig, causal, acc):
     assert bool(np.all(out[empty] == 0)), "rows without keys must be exactly zero"
 
 
-@pytest.mark.parametrize("kernel", [k for k in kernel_ids() if kernel_name(k).startswith("pp_")]
-                         if kernel_ids() != [1] else [])
+@pytest.mark.parametrize("kernel", kernel_ids())
 def test_causal_every_masking_tile(library_path, kernel):
     nq, nk = 600, 900
     say(f"case causal tile {kernel} nq={nq} nk={nk}")

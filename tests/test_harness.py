@@ -1,375 +1,326 @@
-"""Host-only regressions for the plugin API, the drivers and the harness.
+"""Host-only tests of the harness: catalog, drivers, report, kernel attribution, CLI.
 
-Mirror the intent of the reference's host tests
-(tests/test_external_ascendc.py, tests/test_kernel_names.py): driver selection
-and compile policy, the reference backend's exact call, deferred adaptation,
-prepare-before-inputs ordering in the bench, compile-phase task selection,
-project validation and build/load ordering for the hip driver, and exact
-kernel-name attribution in the profiler. Everything runs on the CPU with
-mocks and a synthetic project directory.
+Everything runs on the CPU. Fake backend modules are plain namespaces;
+device work is replaced by CPU tensors and patched timing, so what is tested
+is the protocol: what is loaded when, what is compared with what, what a
+failure turns into.
 """
 
-import subprocess
-import sys
-import tempfile
-import unittest
-from pathlib import Path
+import csv
 from types import SimpleNamespace
 from unittest.mock import Mock, patch
 
-from fa_amd.core import contract, profiler, registry
-from fa_amd.core.drivers import external, hip
+import pytest
+import torch
+
+from fa_amd.harness import drivers, report, timing
+from fa_amd.harness.catalog import Backend, Catalog
+from fa_amd.harness.contract import KernelNameError, Meta
+from fa_amd.problem.cases import CASES, Case
 
 
-class ExternalTests(unittest.TestCase):
-    def test_registration_and_precompile_selection(self):
-        prebuilt = SimpleNamespace(META=SimpleNamespace(type="external"))
-        source = SimpleNamespace(META=prebuilt.META, build=Mock())
-        self.assertIs(registry.driver_for(prebuilt.META), external)
-        self.assertFalse(registry.needs_compile(prebuilt))
-        self.assertTrue(registry.needs_compile(source))
-        self.assertTrue(registry.needs_compile(SimpleNamespace(META=SimpleNamespace(type="hip"))))
-
-    def test_unknown_types_are_rejected(self):
-        for kind in ("torch", "ascendc", "tilelang"):
-            with self.assertRaises(KeyError):
-                registry.driver_for(SimpleNamespace(type=kind))
-
-    def test_reference_backend_uses_external_driver_and_exact_formula_call(self):
-        from fa_amd.backends.torch_ref import backend
-
-        self.assertEqual(backend.META.type, "external")
-        self.assertIs(registry.driver_for(backend.META), external)
-        self.assertFalse(registry.needs_compile(backend))
-        self.assertTrue(backend.META.is_reference)
-        canonical = {name: object() for name in ("q", "k", "v")}
-        case = SimpleNamespace(heads_q=12, scale=0.125)
-        output = object()
-        with patch.object(backend, "attention", Mock(return_value=output)) as attn:
-            external.compile(backend, case)
-            call = external.make_call(backend, case, canonical)
-            attn.assert_not_called()
-            self.assertIs(call(), output)
-            self.assertIs(call(), output)
-        self.assertEqual(attn.call_count, 2)
-        attn.assert_called_with(canonical["q"], canonical["k"], canonical["v"], 0.125)
-
-    def test_reference_backend_formula_on_cpu(self):
-        import torch
-
-        from fa_amd.backends.torch_ref import backend
-
-        g = torch.Generator().manual_seed(0)
-        q = torch.randn(1, 4, 64, 128, generator=g).half()
-        k = torch.randn(1, 2, 96, 128, generator=g).half()
-        v = torch.randn(1, 2, 96, 128, generator=g).half()
-        out = backend.attention(q, k, v, 128 ** -0.5, chunk_elems=96 * 16)
-        sd = torch.nn.functional.scaled_dot_product_attention(
-            q.float(), k.float().repeat_interleave(2, 1), v.float().repeat_interleave(2, 1)).half()
-        self.assertLessEqual(float((out.float() - sd.float()).abs().max()), 2 ** -10)
-
-    def test_optional_build_and_opaque_argument_object(self):
-        args = {"q": "tensor", "custom": 123}
-        spec = SimpleNamespace(adapt=Mock(return_value=args), call=Mock(return_value="out"))
-        external.compile(spec, "case")
-        call = external.make_call(spec, "case", "canonical")
-        spec.adapt.assert_called_once_with("case", "canonical")
-        self.assertEqual(call(), "out")
-        self.assertEqual(call(), "out")
-        self.assertEqual(spec.call.call_count, 2)
-        spec.call.assert_called_with(args)
-        spec.build = Mock()
-        external.compile(spec, "case")
-        external.make_call(spec, "case", "canonical")
-        self.assertEqual(spec.build.call_count, 2)
-
-    def test_generic_prepare_defers_adaptation_until_inputs_exist(self):
-        spec = SimpleNamespace(META=SimpleNamespace(type="external"),
-                               adapt=Mock(return_value="args"), call=Mock(return_value="out"))
-        bind = registry.prepare_call(spec, "case")
-        spec.adapt.assert_not_called()
-        call = bind("canonical")
-        spec.adapt.assert_called_once_with("case", "canonical")
-        self.assertEqual(call(), "out")
-
-    def test_bench_prepares_backends_before_inputs(self):
-        from fa_amd.core import bench
-        from fa_amd.problem import canonical
-
-        events = []
-        spec = SimpleNamespace(META=SimpleNamespace(type="hip", op_type="Test", is_reference=True))
-
-        def prepare(spec, case):
-            events.append("load")
-
-            def bind(inputs):
-                events.append("adapt")
-                return lambda: None
-
-            return bind
-
-        def inputs(case, seed, device=None):
-            events.append("inputs")
-            return {}
-
-        with (
-            patch.object(registry, "get", return_value=spec),
-            patch.object(registry, "prepare_call", side_effect=prepare),
-            patch.object(canonical, "build_canonical", side_effect=inputs),
-            patch.object(bench.torch.cuda, "synchronize", Mock()),
-            patch.object(bench.profiler, "profile_case_us", return_value={"test": 1.0}),
-        ):
-            rows = bench.process_case(0, backend_names=["test"], ref_name="test", iters=1,
-                                      do_check=False, seed=0, atol=0, rtol=0)
-        self.assertEqual(events, ["load", "inputs", "adapt"])
-        self.assertEqual(rows[0][:4], ["B1_S4096_Q12_KV1_D128", "test", "ref", "1.00"])
-
-    def test_bench_skips_a_backend_whose_load_fails(self):
-        from fa_amd.core import bench
-        from fa_amd.problem import canonical
-
-        good = SimpleNamespace(META=SimpleNamespace(type="external", is_reference=True))
-        bad = SimpleNamespace(META=SimpleNamespace(type="hip", is_reference=False))
-        specs = {"good": good, "bad": bad}
-
-        import torch
-
-        def prepare(spec, case):
-            if spec is bad:
-                raise FileNotFoundError("artifacts missing")
-            return lambda inputs: (lambda: torch.zeros(2))
-
-        with (
-            patch.object(registry, "get", side_effect=specs.__getitem__),
-            patch.object(registry, "prepare_call", side_effect=prepare),
-            patch.object(canonical, "build_canonical", return_value={}),
-            patch.object(bench.torch.cuda, "synchronize", Mock()),
-            patch.object(bench.profiler, "profile_case_us",
-                         return_value={"good": 2.0, "bad": None}),
-        ):
-            rows = bench.process_case(0, backend_names=["good", "bad"], ref_name="good",
-                                      iters=1, do_check=True, seed=0, atol=0, rtol=0)
-        verdict = {r[1]: r[5] for r in rows}
-        self.assertEqual(verdict, {"good": "ref", "bad": "ERR"})
-
-    def test_kernel_name_errors_are_not_swallowed(self):
-        from fa_amd.core import bench
-
-        spec = SimpleNamespace(META=SimpleNamespace(type="hip"))
-        with (
-            patch.object(registry, "get", return_value=spec),
-            patch.object(registry, "prepare_call",
-                         side_effect=contract.KernelNameError("bad symbol")),
-        ):
-            with self.assertRaises(contract.KernelNameError):
-                bench.process_case(0, backend_names=["x"], ref_name="x", iters=1,
-                                   do_check=False, seed=0, atol=0, rtol=0)
-
-    def test_bench_selects_source_external_and_hip_projects(self):
-        from fa_amd.core import bench
-
-        specs = {
-            name: SimpleNamespace(META=SimpleNamespace(type=kind))
-            for name, kind in (("prebuilt", "external"), ("source", "external"),
-                               ("project", "hip"), ("torch_op", "external"))
-        }
-        specs["source"].build = Mock()
-        seen = []
-
-        def collect(tasks, worker):
-            seen.extend(tasks)
-            return []
-
-        with (
-            patch.object(registry, "_BACKENDS", specs),
-            patch.object(bench.schedule, "parallel_compile", side_effect=collect),
-        ):
-            bench.compile_phase(list(specs), [0, 1])
-        self.assertEqual(seen, [("source", 0), ("source", 1), ("project", 0), ("project", 1)])
+def fake(name, kind="external", ref=False, diagnostic=False, **hooks):
+    module = SimpleNamespace(__name__=f"fake.{name}",
+                             META=Meta(name=name, type=kind, op_type=f"{name}_op",
+                                       is_reference=ref, diagnostic=diagnostic),
+                             **hooks)
+    return Backend(name, module)
 
 
-class RegistryTests(unittest.TestCase):
-    def test_discovery_keys_by_directory_with_one_reference(self):
-        names = registry.all_names()
-        self.assertEqual(sorted(names), ["hip_fa_fp16acc", "hip_fa_fp32acc", "torch_ref"])
-        ref_name, ref = registry.get_reference()
-        self.assertEqual(ref_name, "torch_ref")
-        for n in names:
-            self.assertEqual(registry.name_of(registry.get(n)), n)
-
-    def test_registry_rejects_unregistered_or_ambiguous_module(self):
-        spec = SimpleNamespace(META=SimpleNamespace(diagnostic=False))
-        for registered in ({}, {"one": spec, "two": spec}):
-            with patch.object(registry, "_BACKENDS", registered):
-                with self.assertRaises(ValueError):
-                    registry.name_of(spec)
-
-    def test_reference_must_be_unique(self):
-        ref = SimpleNamespace(META=SimpleNamespace(is_reference=True))
-        for registered in ({}, {"a": ref, "b": ref}):
-            with patch.object(registry, "_BACKENDS", registered):
-                with self.assertRaises(ValueError):
-                    registry.get_reference()
-
-    def test_diagnostic_backends_are_not_attention(self):
-        diag = SimpleNamespace(META=SimpleNamespace(diagnostic=True))
-        with patch.object(registry, "_BACKENDS", {"diag": diag}):
-            self.assertEqual(registry.all_names(), [])
-            self.assertEqual(registry.all_names(include_diagnostics=True), ["diag"])
-            with self.assertRaisesRegex(ValueError, "diagnostic"):
-                registry.require_attention(diag)
-
-    def test_hip_backends_declare_kernel_symbols_containing_their_names(self):
-        for n in ("hip_fa_fp32acc", "hip_fa_fp16acc"):
-            meta = registry.get(n).META
-            self.assertEqual(meta.type, "hip")
-            self.assertTrue(meta.op_type.startswith(n))
+def catalog_of(*entries):
+    return Catalog({e.name: e for e in entries})
 
 
-class HipProjectTests(unittest.TestCase):
-    def setUp(self):
-        self.temp = tempfile.TemporaryDirectory()
-        self.addCleanup(self.temp.cleanup)
-        self.root = Path(self.temp.name)
-        (self.root / "csrc").mkdir()
-        (self.root / "csrc" / "op.hip").write_text("// structure fixture, not a kernel\n")
+# --------------------------------------------------------------------------- catalog
 
-    def spec(self, command=()):
-        project = hip.Project(self.root, ("build/libop.so",), command)
-        operator = Mock(return_value="canonical output")
-        return SimpleNamespace(project=Mock(return_value=project),
-                               load=Mock(return_value=operator),
-                               adapt=Mock(return_value=("q", "k", "v")))
-
-    def test_generic_backend_is_rejected(self):
-        spec = SimpleNamespace(adapt=Mock(), call=Mock())
-        with self.assertRaisesRegex(TypeError, 'type="external"'):
-            hip.compile(spec, "case")
-        spec.adapt.assert_not_called()
-        spec.call.assert_not_called()
-
-    def test_prepare_loads_without_adapting_or_launching(self):
-        (self.root / "build").mkdir()
-        (self.root / "build/libop.so").write_bytes(b"test fixture")
-        spec = self.spec()
-        spec.META = SimpleNamespace(type="hip")
-        bind = registry.prepare_call(spec, "case")
-        spec.load.assert_called_once()
-        spec.adapt.assert_not_called()
-        spec.load.return_value.assert_not_called()
-        call = bind("canonical")
-        spec.adapt.assert_called_once_with("case", "canonical")
-        self.assertEqual(call(), "canonical output")
-
-    def test_structural_validation_precedes_build(self):
-        (self.root / "csrc" / "op.hip").unlink()
-        with patch.object(hip.subprocess, "run") as run:
-            with self.assertRaisesRegex(ValueError, "csrc"):
-                hip.compile(self.spec(("unused",)), "case")
-            run.assert_not_called()
-
-    def test_explicit_build_outputs_load_and_call(self):
-        command = (sys.executable, "-c",
-                   "from pathlib import Path; Path('build').mkdir(exist_ok=True); "
-                   "Path('build/libop.so').write_bytes(b'host-test artifact, not ELF')")
-        spec = self.spec(command)
-        hip.compile(spec, "case")
-        self.assertTrue((self.root / "build/libop.so").is_file())
-        spec.load.assert_not_called()  # the CPU build never loads the library
-        call = hip.make_call(spec, "case", "canonical")
-        spec.load.assert_called_once_with("case", spec.project.return_value)
-        spec.adapt.assert_called_once_with("case", "canonical")
-        self.assertEqual(call(), "canonical output")
-        spec.load.return_value.assert_called_once_with("q", "k", "v")
-
-    def test_prebuilt_project_requires_declared_outputs(self):
-        spec = self.spec()
-        with self.assertRaises(FileNotFoundError):
-            hip.make_call(spec, "case", "canonical")
-        spec.load.assert_not_called()
-        (self.root / "build").mkdir()
-        (self.root / "build/libop.so").write_bytes(b"fixture")
-        with patch.object(hip.subprocess, "run") as run:
-            hip.compile(spec, "case")
-            run.assert_not_called()
-
-    def test_failed_build_never_loads_or_runs(self):
-        spec = self.spec((sys.executable, "-c", "raise SystemExit(3)"))
-        with self.assertRaises(subprocess.CalledProcessError):
-            hip.make_call(spec, "case", "canonical")
-        spec.load.assert_not_called()
-        spec.adapt.assert_not_called()
-
-    def test_invalid_recipe_and_escaping_artifacts_rejected(self):
-        for project in (hip.Project(self.root, ("../escape.so",)),
-                        hip.Project(self.root, ("/absolute.so",)),
-                        hip.Project(self.root, ()),
-                        hip.Project(self.root, ("build/lib.so",), "bash build.sh"),
-                        hip.Project(self.root, ("build/lib.so",), (), 0)):
-            with self.subTest(project=project), self.assertRaises((ValueError, TypeError)):
-                project.validate()
-
-    def test_binding_and_argument_contracts_checked(self):
-        (self.root / "build").mkdir()
-        (self.root / "build/libop.so").write_bytes(b"fixture")
-        spec = self.spec()
-        spec.load.return_value = None
-        with self.assertRaisesRegex(TypeError, "callable binding"):
-            hip.make_call(spec, "case", "canonical")
-        spec.load.return_value = Mock()
-        spec.adapt.return_value = {"q": "not a tuple"}
-        with self.assertRaisesRegex(TypeError, "positional-argument tuple"):
-            hip.make_call(spec, "case", "canonical")
-
-    def test_real_project_recipe_is_valid_and_needs_no_process_when_current(self):
-        from fa_amd import build
-        from fa_amd.backends import hip_common
-
-        project = hip_common.project(None)
-        project.validate()
-        if build.up_to_date():
-            self.assertEqual(project.build_command, ())
+def test_package_catalog_has_three_backends_and_one_reference():
+    cat = Catalog.default(rescan=True)
+    assert sorted(cat.names()) == ["hip_fa_fp16acc", "hip_fa_fp32acc", "torch_ref"]
+    assert cat.reference.name == "torch_ref"
+    for n in cat.names():
+        entry = cat[n]
+        assert cat.name_of(entry.module) == n
+        assert entry.driver.kind == entry.meta.type
+    for n in ("hip_fa_fp32acc", "hip_fa_fp16acc"):
+        assert cat[n].meta.type == "hip" and cat[n].meta.op_type == f"{n}_kernel"
 
 
-class ProfileNameTests(unittest.TestCase):
-    def test_exact_symbols_disambiguate_prefixes(self):
-        names = ["hip_fa", "hip_fa_v3", "torch_ref"]
-        symbols = {n: f"{n}_kernel" for n in names[:2]}
-        op_types = {n: "main_kernel" for n in names[:2]}
-        op_types["torch_ref"] = "Cijk"
-        expected = {
-            "hip_fa_kernel": "hip_fa",
-            "hip_fa_v3_kernel": "hip_fa_v3",
-            "main_kernel": None,
-            "hip_fa_v30_kernel": None,
-            "prefix_hip_fa_v3_kernel": None,
-            "Cijk_Alik_Bljk_S": "torch_ref",
-        }
-        for symbol, backend in expected.items():
-            with self.subTest(symbol=symbol):
-                self.assertEqual(profiler._match_backend(symbol, names, op_types, symbols), backend)
-
-    def test_mangled_hip_kernels_attribute_by_directory_name(self):
-        names = ["hip_fa_fp32acc", "hip_fa_fp16acc", "torch_ref"]
-        op_types = {n: registry.get(n).META.op_type for n in names}
-        k32 = "_ZN12_GLOBAL__N_121hip_fa_fp32acc_kernelILi1ELi2ELi1ELi128ELi2EEEvPKDF16_S2_S2_PDF16_iiiif"
-        k16 = k32.replace("fp32acc", "fp16acc")
-        self.assertEqual(profiler._match_backend(k32, names, op_types, {}), "hip_fa_fp32acc")
-        self.assertEqual(profiler._match_backend(k16, names, op_types, {}), "hip_fa_fp16acc")
-        self.assertIsNone(profiler._match_backend("fa_prep_kernel", names, op_types, {}))
-
-    def test_kernel_trace_averages(self):
-        with tempfile.NamedTemporaryFile("w", suffix=".csv", delete=False) as f:
-            f.write('"Kernel_Name","Start_Timestamp","End_Timestamp"\n')
-            f.write('"x_hip_fa_fp32acc_kernel_y",1000,3000\n"x_hip_fa_fp32acc_kernel_y",5000,9000\n')
-            f.write('"other",0,100\n')
-        got = profiler.kernel_times_us(f.name, ["hip_fa_fp32acc", "torch_ref"])
-        Path(f.name).unlink()
-        self.assertEqual(got, {"hip_fa_fp32acc": 3.0, "torch_ref": None})
+@pytest.mark.parametrize("refs", [0, 2])
+def test_catalog_needs_exactly_one_reference(refs):
+    entries = [fake(f"b{i}", ref=i < refs) for i in range(3)]
+    with pytest.raises(ValueError, match="exactly one reference"):
+        catalog_of(*entries)
 
 
-if __name__ == "__main__":
-    unittest.main()
+def test_unknown_backend_type_and_name():
+    cat = catalog_of(fake("r", ref=True), fake("t", kind="tilelang"))
+    with pytest.raises(drivers.UnknownBackendType):
+        cat["t"].driver
+    with pytest.raises(KeyError, match="no backend 'x'"):
+        cat["x"]
+
+
+def test_diagnostic_backends_are_listed_but_never_checked():
+    cat = catalog_of(fake("r", ref=True), fake("probe", diagnostic=True))
+    assert cat.names() == ["r"]
+    assert cat.names(include_diagnostic=True) == ["r", "probe"]
+    with pytest.raises(ValueError, match="diagnostic"):
+        cat.attention("probe")
+
+
+def test_name_of_rejects_unknown_or_doubly_registered_modules():
+    r, b = fake("r", ref=True), fake("b")
+    cat = catalog_of(r, b, Backend("alias", b.module))
+    with pytest.raises(ValueError):
+        cat.name_of(b.module)
+    assert cat.name_of(r.module) == "r"
+    with pytest.raises(ValueError):
+        cat.name_of(SimpleNamespace(__name__="stranger"))
+
+
+# --------------------------------------------------------------------------- drivers
+
+def test_external_driver_adapts_late_and_calls_every_time():
+    events = []
+    module = SimpleNamespace(__name__="m",
+                             build=lambda case: events.append(("build", case)),
+                             adapt=lambda case, inputs: events.append(("adapt", inputs)) or "args",
+                             call=lambda args: events.append(("call", args)) or "out")
+    d = drivers.driver("external")
+    assert d.needs_build(module)
+    bind = d.prepare(module, "case")
+    assert events == [("build", "case")]
+    forward = bind("inputs")
+    assert events[-1] == ("adapt", "inputs")
+    assert forward() == "out" and forward() == "out"
+    assert events.count(("call", "args")) == 2
+
+
+def test_external_driver_without_build_and_with_a_broken_one():
+    d = drivers.driver("external")
+    plain = SimpleNamespace(__name__="m", adapt=Mock(return_value=1), call=Mock(return_value=2))
+    assert not d.needs_build(plain)
+    assert d.prepare(plain, "case")("inputs")() == 2
+    plain.call.assert_called_once_with(1)
+    broken = SimpleNamespace(__name__="m", build="not callable", adapt=Mock(), call=Mock())
+    with pytest.raises(TypeError):
+        d.prepare(broken, "case")
+
+
+def test_hip_driver_loads_before_inputs_and_checks_hooks():
+    d = drivers.driver("hip")
+    forward = Mock(return_value="o")
+    module = SimpleNamespace(__name__="m", operator=Mock(return_value=forward),
+                             adapt=Mock(return_value=("q", "k", "v")))
+    with patch("fa_amd.build.build") as build:
+        bind = d.prepare(module, "case")
+        build.assert_called_once()
+    module.operator.assert_called_once_with("case")
+    module.adapt.assert_not_called()
+    call = bind("canonical")
+    module.adapt.assert_called_once_with("case", "canonical")
+    assert call() == "o"
+    forward.assert_called_once_with("q", "k", "v")
+
+    with patch("fa_amd.build.build"):
+        with pytest.raises(TypeError, match="missing operator"):
+            d.prepare(SimpleNamespace(__name__="m", adapt=Mock()), "case")
+        module.operator.return_value = None
+        with pytest.raises(TypeError, match="callable"):
+            d.prepare(module, "case")
+        module.operator.return_value = forward
+        module.adapt.return_value = {"q": 1}
+        with pytest.raises(TypeError, match="tuple"):
+            d.prepare(module, "case")("canonical")
+
+
+def test_hip_backends_load_the_built_library_only():
+    from fa_amd import build
+    from fa_amd.backends import hip_common
+
+    with patch.object(build, "LIBRARY", build.LIBDIR / "missing.so"):
+        with pytest.raises(FileNotFoundError):
+            hip_common.operator("fp32", CASES[0])
+
+
+# --------------------------------------------------------------------------- reference backend
+
+def test_reference_backend_is_the_fp32_formula():
+    from fa_amd.backends.torch_ref import backend
+
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(2, 6, 40, 128, generator=g).half()
+    k = torch.randn(2, 3, 72, 128, generator=g).half()
+    v = torch.randn(2, 3, 72, 128, generator=g).half()
+    case = SimpleNamespace(heads_q=6, scale=0.1)
+    out = backend.call(backend.adapt(case, {"q": q, "k": k, "v": v}))
+    ke, ve = k.float().repeat_interleave(2, 1), v.float().repeat_interleave(2, 1)
+    want = torch.softmax(q.float() @ ke.transpose(-1, -2) * 0.1, -1) @ ve
+    assert out.dtype == torch.float16 and out.shape == q.shape
+    assert float((out.float() - want).abs().max()) <= 2 ** -10
+    small = backend.attention(q, k, v, 0.1, chunk_elems=72 * 7)     # ragged row chunks
+    assert float((small.float() - want).abs().max()) <= 2 ** -10
+
+
+# --------------------------------------------------------------------------- report
+
+def run_report(entries, case=CASES[0], **kw):
+    cat = catalog_of(*entries)
+    inputs = {"q": torch.ones(1)}
+    with patch("fa_amd.problem.canonical.build_canonical", return_value=inputs) as draw, \
+            patch.object(torch.cuda, "synchronize"), \
+            patch.object(timing, "device_us", return_value=50.0):
+        rows = report.run_case(cat, case, [e.name for e in entries], device="cpu",
+                               log=lambda *_: None, **kw)
+    return rows, draw
+
+
+def test_report_prepares_everything_before_drawing_inputs():
+    events = []
+
+    def module(name, out):
+        return SimpleNamespace(
+            __name__=name,
+            build=lambda case: events.append(f"build {name}"),
+            adapt=lambda case, inputs: events.append(f"adapt {name}") or None,
+            call=lambda args: out)
+
+    ref = Backend("ref", module("ref", torch.zeros(4)))
+    ref.module.META = Meta("ref", "external", "ref", is_reference=True)
+    mine = Backend("mine", module("mine", torch.full((4,), 0.005)))
+    mine.module.META = Meta("mine", "external", "mine")
+
+    def draw(*a, **k):
+        events.append("inputs")
+        return {}
+
+    cat = catalog_of(ref, mine)
+    with patch("fa_amd.problem.canonical.build_canonical", side_effect=draw), \
+            patch.object(torch.cuda, "synchronize"), \
+            patch.object(timing, "device_us", side_effect=[100.0, 25.0]):
+        rows = report.run_case(cat, CASES[0], ["mine"], device="cpu", log=lambda *_: None)
+    assert events == ["build ref", "build mine", "inputs", "adapt ref", "adapt mine"]
+    by = {r.backend: r for r in rows}
+    assert by["ref"].check == "ref" and by["mine"].check == "PASS"
+    assert by["mine"].max_diff == pytest.approx(0.005)
+    assert by["mine"].vs_ref == pytest.approx(0.25)
+    cells = by["mine"].cells()
+    assert cells[:6] == ["B1_S4096_Q12_KV1_D128", "mine", "", "25.00", "25.0%", "PASS"]
+    assert float(cells[7]) == pytest.approx(CASES[0].flops / 25e-6 / 1e12, rel=1e-3)
+
+
+def test_report_fails_a_wrong_backend_and_skips_a_broken_one():
+    ref = fake("ref", ref=True, adapt=Mock(), call=Mock(return_value=torch.zeros(8)))
+    wrong = fake("wrong", adapt=Mock(), call=Mock(return_value=torch.full((8,), 0.5)))
+    broken = fake("broken", build=Mock(side_effect=OSError("no library")), adapt=Mock(),
+                  call=Mock())
+    crashing = fake("crashing", adapt=Mock(), call=Mock(side_effect=RuntimeError("launch")))
+    rows, _ = run_report([ref, wrong, broken, crashing])
+    by = {r.backend: r for r in rows}
+    assert by["wrong"].check == "FAIL" and by["wrong"].max_diff == pytest.approx(0.5)
+    assert by["broken"].check == "ERR" and by["broken"].avg_us is None
+    assert by["crashing"].check == "ERR"
+    assert by["broken"].cells()[3] == "N/A"
+    broken.module.call.assert_not_called()
+
+
+def test_report_never_swallows_kernel_name_errors():
+    ref = fake("ref", ref=True, adapt=Mock(), call=Mock(return_value=torch.zeros(1)))
+    bad = fake("bad", adapt=Mock(), call=Mock(side_effect=KernelNameError("unnamed kernel")))
+    with pytest.raises(KernelNameError):
+        run_report([ref, bad])
+
+
+def test_check_backend_compares_with_the_reference():
+    ref = fake("ref", ref=True, adapt=Mock(), call=Mock(return_value=torch.zeros(3)))
+    close = fake("close", adapt=Mock(), call=Mock(return_value=torch.tensor([0., 0.004, 0.])))
+    cat = catalog_of(ref, close)
+    with patch("fa_amd.problem.canonical.build_canonical", return_value={}):
+        assert report.check_backend(cat, "close", CASES[0], device="cpu") == (True, pytest.approx(0.004))
+        assert report.check_backend(cat, "ref", CASES[0], device="cpu") == (True, 0.0)
+        passed, diff = report.check_backend(cat, "close", CASES[0], device="cpu",
+                                            tol=report.Tolerance(1e-3, 0.0))
+    assert not passed and diff == pytest.approx(0.004)
+    line = report.check_line(CASES[3], "close", False, 0.004)
+    assert line == ("CHECK B2_S131072_Q12_KV1_D128 backend=close FAIL max_abs_diff=0.00400 "
+                    "(atol=0.01, rtol=0.01)")
+
+
+def test_report_csv_has_the_reference_columns_first(tmp_path):
+    rows = [report.Row("c", "b", False, 10.0, 0.5, "PASS", 1e-4, 3.0)]
+    path = tmp_path / "r.csv"
+    report.write_csv(rows, path)
+    head, body = list(csv.reader(open(path)))
+    assert head[:7] == ["Case", "Backend", "Ref", "Avg_us", "vs_ref", "Check", "MaxDiff"]
+    assert body == ["c", "b", "", "10.00", "50.0%", "PASS", "0.00010", "3.0", "0.1%"]
+
+
+# --------------------------------------------------------------------------- kernel attribution
+
+def test_declared_symbols_match_exactly_and_only_exactly():
+    owners = KernelOwnersCase.owners()
+    for kernel, backend in KernelOwnersCase.EXPECTED.items():
+        assert owners.owner(kernel) == backend, kernel
+
+
+class KernelOwnersCase:
+    EXPECTED = {
+        "attn_kernel": "attn",                        # default exact symbol <dir>_kernel
+        "attn_v2_kernel": "attn_v2",                  # exact beats attn's substring
+        "fast_main": "fast",                          # declared symbol
+        "fast_main_v2": None,                         # declared backends never match loosely
+        "fast_kernel": None,                          # ... not even by the default symbol
+        "FlashAttentionScore_1": "vendor",            # op_type substring
+        "xx_vendor_yy": "vendor",                     # directory-name substring
+        "attn_kernel_tail": "attn",                   # substring for undeclared backends
+        "unrelated": None,
+    }
+
+    @staticmethod
+    def owners():
+        return timing.KernelOwners(["attn", "attn_v2", "fast", "vendor"],
+                                   op_types={"vendor": "FlashAttentionScore", "fast": "main"},
+                                   symbols={"fast": "fast_main"})
+
+
+def test_hip_kernels_are_attributed_to_their_backend(tmp_path):
+    cat = Catalog.default()
+    names = ["hip_fa_fp32acc", "hip_fa_fp16acc", "torch_ref"]
+    owners = timing.KernelOwners(names, op_types={n: cat[n].meta.op_type for n in names})
+    mangled = "_ZN12_GLOBAL__N_121hip_fa_fp32acc_kernelILi1ELi2ELi1ELi128ELi2ELb0EEEvNS_6FaArgsE"
+    assert owners.owner(mangled) == "hip_fa_fp32acc"
+    assert owners.owner(mangled.replace("fp32acc", "fp16acc")) == "hip_fa_fp16acc"
+    assert owners.owner("_ZN12_GLOBAL__N_114fa_prep_kernelEPKDF16_") is None
+    trace = tmp_path / "kernel_trace.csv"
+    trace.write_text('"Kernel_Name","Start_Timestamp","End_Timestamp"\n'
+                     f'"{mangled}",1000,3000\n"{mangled}",5000,9000\n"other",0,100\n')
+    assert owners.average_us(trace) == {"hip_fa_fp32acc": 3.0, "hip_fa_fp16acc": None,
+                                        "torch_ref": None}
+
+
+# --------------------------------------------------------------------------- CLI
+
+def test_cli_names_configurations_by_c_index_or_case_name():
+    from fa_amd.harness.__main__ import resolve_cases
+
+    assert resolve_cases("c3") == [CASES[3]]
+    assert resolve_cases("c0, B2_S65536_Q12_KV1_D128_stress,c0") == [CASES[0], CASES[4]]
+    assert resolve_cases("all") == list(CASES)
+    for bad in ("3", "c9", "B9_S1", ""):
+        with pytest.raises(SystemExit):
+            resolve_cases(bad)
+
+
+def test_cli_list_and_build(capsys):
+    from fa_amd.harness.__main__ import main
+
+    assert main(["list"]) == 0
+    out = capsys.readouterr().out
+    assert "c3  B2_S131072_Q12_KV1_D128" in out and "backend torch_ref: type=external (reference)" in out
+    with patch("fa_amd.build.build") as build:
+        assert main(["build", "--backend", "hip_fa_fp32acc"]) == 0
+        build.assert_called_once()
+    assert "BUILD hip_fa_fp32acc done" in capsys.readouterr().out
 
 
 def test_visible_pairs_counts_masked_flops():
@@ -387,3 +338,4 @@ def test_visible_pairs_counts_masked_flops():
                 assert visible_pairs(nq, nk, causal) == brute(nq, nk, causal), (nq, nk, causal)
     n = 131072
     assert visible_pairs(n, n, "top_left") == n * (n + 1) // 2
+    assert Case(1, 8, 2, 1).flops == 4 * 2 * 8 * 8 * 128

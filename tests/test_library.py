@@ -58,10 +58,9 @@ def test_workspace_size(lib):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(batch=0), 2), (dict(heads_q=12, heads_kv=5), 2), (dict(seq_k=-64), 2),
-    (dict(dim=64), 3), (dict(seq_q=4000, kernel=1), 4), (dict(seq_k=4100, kernel=2), 4),
-    (dict(acc=2), 7), (dict(scale=0.0), 8), (dict(scale=float("inf")), 8),
-    (dict(kernel=99), 9), (dict(causal=3), 12), (dict(causal=-1), 12), (dict(seq_q=1 << 30), 2),
-    (dict(causal=1, kernel=1), 12), (dict(causal=2, kernel=2), 12),
+    (dict(dim=64), 3), (dict(acc=2), 7), (dict(scale=0.0), 8), (dict(scale=float("inf")), 8),
+    (dict(kernel=99), 9), (dict(kernel=-1), 9), (dict(causal=3), 12), (dict(causal=-1), 12),
+    (dict(seq_q=1 << 30), 2),
 ])
 def test_geometry_errors(lib, kw, code):
     rc, _ = ws_bytes(lib, problem(**kw))
@@ -80,19 +79,17 @@ def test_ragged_tails_and_workspace(lib):
         assert size == 2 * pad * 128 * 2, (nq, nk, size)
     rc, size = ws_bytes(lib, problem(seq_q=300, seq_k=4096))
     assert rc == 0 and size == 4096 * 128 * 2          # no key tail: V^T only
-    for kernel in (1, 2):                              # plain tiles keep exact tiling
-        assert ws_bytes(lib, problem(seq_q=300, kernel=kernel))[0] == 4
+    # A 64-key tile pads to whole 64-key blocks.
+    rc, size = ws_bytes(lib, problem(seq_q=300, seq_k=1000, kernel=1))
+    assert rc == 0 and size == 2 * 1024 * 128 * 2
+    for kernel in range(lib.fa_kernel_count() + 1):      # every tile masks tails
         rows, keys = C.c_int32(), C.c_int32()
         assert lib.fa_fwd_tile(C.byref(problem(kernel=kernel)), C.byref(rows), C.byref(keys)) == 0
-        assert rows.value >= 64 and keys.value == 64
-    rows, keys = C.c_int32(), C.c_int32()
-    assert lib.fa_fwd_tile(C.byref(problem()), C.byref(rows), C.byref(keys)) == 0
-    assert (rows.value, keys.value) == (1, 1)
+        assert (rows.value, keys.value) == (1, 1)
 
 
 def test_causal_selection(lib):
-    # Causal masks run on the masking (ping-pong) tiles only: the automatic
-    # choice picks one whatever the shape, explicit plain tiles are refused.
+    # Every tile applies causal masks, whatever the shape.
     for causal in (1, 2):
         for nq, nk in ((4096, 4096), (300, 1000), (1000, 7)):
             for acc in (0, 1):
@@ -101,7 +98,7 @@ def test_causal_selection(lib):
                 assert lib.fa_fwd_select(C.byref(prob), C.byref(idx)) == 0
                 assert lib.fa_kernel_name(idx.value).startswith(b"pp_"), (causal, nq, nk, acc)
                 assert ws_bytes(lib, prob)[0] == 0
-        for kernel in (3, 4, 5):
+        for kernel in range(1, lib.fa_kernel_count() + 1):
             assert ws_bytes(lib, problem(causal=causal, kernel=kernel))[0] == 0
     assert b"causal" in lib.fa_strerror(12)
     with pytest.raises(ValueError):
@@ -124,8 +121,6 @@ def test_capture_count_and_rejections(lib):
     prob16 = problem(seq_q=300, seq_k=1000, acc=1)   # FP16 default tile: 64-key blocks
     assert lib.fa_fwd_capture_count(C.byref(prob16), C.byref(count), C.byref(block)) == 0
     assert block.value == 64 and count.value == 4 * 16 * 12 * 300
-    plain = problem(kernel=1)                        # plain tiles have no capture mode
-    assert lib.fa_fwd_capture_count(C.byref(plain), C.byref(count), C.byref(block)) == 11
     assert lib.fa_fwd_capture_count(C.byref(prob), None, C.byref(block)) == 1
     # Launch-time checks happen on the host, before any GPU work.
     p = C.c_void_p(4096)
@@ -133,9 +128,26 @@ def test_capture_count_and_rejections(lib):
     need = 4 * 8 * 12 * 300
     assert lib.fa_fwd_capture(C.byref(prob), p, p, p, p, None, None, need, p, size, None) == 1
     assert lib.fa_fwd_capture(C.byref(prob), p, p, p, p, None, p, need - 1, p, size, None) == 11
-    _, psize = ws_bytes(lib, plain)
-    assert lib.fa_fwd_capture(C.byref(plain), p, p, p, p, None, p, 1 << 40, p, psize, None) == 11
     assert lib.fa_strerror(11)
+
+
+def test_trace_count_and_rejections(lib):
+    # One 8-word record per workgroup: B * Hq * ceil(Nq / 256) workgroups.
+    prob = problem(batch=2, seq_q=300, seq_k=1000)
+    count = C.c_uint64()
+    assert lib.fa_fwd_trace_count(C.byref(prob), C.byref(count)) == 0
+    assert count.value == 8 * 2 * 12 * 2
+    assert lib.fa_fwd_trace_count(C.byref(prob), None) == 1
+    assert lib.fa_fwd_trace_count(C.byref(problem(dim=64)), C.byref(count)) == 3
+    p = C.c_void_p(4096)
+    _, size = ws_bytes(lib, prob)
+    need = 8 * 2 * 12 * 2
+    assert lib.fa_fwd_trace(C.byref(prob), p, p, p, p, None, need, p, size, None) == 1
+    assert lib.fa_fwd_trace(C.byref(prob), p, p, p, p, p, need - 1, p, size, None) == 13
+    assert lib.fa_fwd_trace(C.byref(prob), p, p, p, p, C.c_void_p(4104), need, p, size, None) == 5
+    assert b"trace" in lib.fa_strerror(13)
+    with pytest.raises(ValueError):
+        binding.AttentionConfig(trace=True, capture=True)
 
 
 def test_fwd_rejects_before_launch(lib):
@@ -156,14 +168,14 @@ def test_fwd_rejects_before_launch(lib):
 
 def test_kernel_table(lib):
     n = lib.fa_kernel_count()
-    assert n >= 1
+    assert n == 3
     names = [lib.fa_kernel_name(i).decode() for i in range(1, n + 1)]
     assert len(set(names)) == n
     assert lib.fa_kernel_name(0) is None and lib.fa_kernel_name(n + 1) is None
     for i in range(0, n + 1):
         rows, keys = C.c_int32(), C.c_int32()
         assert lib.fa_fwd_tile(C.byref(problem(kernel=i)), C.byref(rows), C.byref(keys)) == 0
-        assert (rows.value, keys.value) == (1, 1) or (rows.value % 32 == 0 and keys.value % 32 == 0)
+        assert (rows.value, keys.value) == (1, 1)
         sel = C.c_int32()
         assert lib.fa_fwd_select(C.byref(problem(kernel=i)), C.byref(sel)) == 0
         assert (sel.value == i) if i else (1 <= sel.value <= n)
@@ -172,18 +184,14 @@ def test_kernel_table(lib):
     assert lib.fa_fwd_select(None, C.byref(sel)) == 1
 
 
-def test_automatic_choice_fits_the_problem(lib):
-    # kernel = 0 picks a tile whose granularity divides the problem; the
-    # headline shape gets the 128-key ping-pong tile.
-    for seq in (4096, 32768, 131072, 512, 768):
-        prob = problem(seq_q=seq, seq_k=seq)
-        sel, rows, keys = C.c_int32(), C.c_int32(), C.c_int32()
-        assert lib.fa_fwd_select(C.byref(prob), C.byref(sel)) == 0
-        assert lib.fa_fwd_tile(C.byref(prob), C.byref(rows), C.byref(keys)) == 0
-        assert seq % rows.value == 0 and seq % keys.value == 0, (seq, sel.value)
-    prob = problem(batch=2, seq_q=131072, seq_k=131072)
-    assert lib.fa_fwd_select(C.byref(prob), C.byref(sel)) == 0
-    assert lib.fa_kernel_name(sel.value) == b"pp_n128_r2"
+def test_automatic_choice(lib):
+    # kernel = 0: the 128-key tile for FP32 O, the 3-slot 64-key ring for FP16 O.
+    sel = C.c_int32()
+    for seq in (4096, 131072, 1000):
+        assert lib.fa_fwd_select(C.byref(problem(seq_q=seq, seq_k=seq)), C.byref(sel)) == 0
+        assert lib.fa_kernel_name(sel.value) == b"pp_n128_r2"
+        assert lib.fa_fwd_select(C.byref(problem(seq_q=seq, seq_k=seq, acc=1)), C.byref(sel)) == 0
+        assert lib.fa_kernel_name(sel.value) == b"pp_n64_r3"
 
 
 def test_operator_validation_without_gpu(library_path):
@@ -199,9 +207,6 @@ def test_operator_validation_without_gpu(library_path):
            torch.zeros(1, 5, 256, 128, dtype=torch.float16))
     with pytest.raises(ValueError, match=r"\[B,H,N,128\]"):
         op(q[0], k, k)
-    plain = binding.Operator(library_path, binding.AttentionConfig(kernel=1))
-    with pytest.raises(ValueError, match="tail"):
-        plain(q[:, :, :200], k, k)
     with pytest.raises(ValueError):
         binding.AttentionConfig(acc="bf16")
 

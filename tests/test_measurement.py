@@ -6,7 +6,7 @@ import sqlite3
 
 import pytest
 
-from fa_amd.core import kernel_stats, traffic
+from fa_amd.measure import kernel_stats, traffic
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -80,7 +80,7 @@ def test_bench_reads_the_committed_traffic_summary():
 
 
 def test_counter_summary(tmp_path):
-    from fa_amd.core import counters
+    from fa_amd.measure import counters
 
     write_counters(tmp_path / "c", "SQ_BUSY_CYCLES", [(1, "hip_fa_fp32acc_kernel", 5.0),
                                                       (1, "hip_fa_fp32acc_kernel", 7.0),
@@ -100,3 +100,28 @@ def test_bench_cli_contract():
     assert bench.parse_args(["--causal", "bottom_right"]).causal == "bottom_right"
     # More than one GPU is refused before anything touches a device.
     assert bench.main(["--gpus", "2"]) == 2
+
+
+def test_clock_summary_from_trace_records():
+    import numpy as np
+
+    from fa_amd.measure import clock
+
+    # Two workgroups on die 1 at 1500 MHz, one on die 3 at 2000 MHz, one empty record.
+    rec = np.zeros((4, 8), dtype=np.int64)
+    rec[0] = [(1 << 32) | 5, 1000, 2000, 10, 10 + 15_000, 0, 8, 128]     # 1000 ticks = 10 us
+    rec[1] = [(1 << 32) | 6, 1000, 3000, 50, 50 + 30_000, 1, 8, 128]
+    rec[2] = [(3 << 32) | 7, 500, 1500, 0, 20_000, 2, 8, 128]
+    rec[3] = [0, 7, 7, 0, 0, 3, 0, 128]
+    assert np.allclose(clock.clocks_mhz(rec), [1500, 1500, 2000])
+    s = clock.summarize(rec)
+    assert s["workgroups"] == 4 and s["median_mhz"] == 1500
+    assert s["per_xcc_median_mhz"] == {1: 1500.0, 3: 2000.0}
+    # Weighted by each record's span: (1500*1000 + 1500*2000 + 2000*1000) / 4000.
+    assert s["mean_mhz_time_weighted"] == pytest.approx(1625.0)
+    assert s["span_ms"] == pytest.approx((3000 - 7) / 1e5)        # first entry: the empty record
+    assert clock.roof_at(1200.0) == pytest.approx(2516.6 / 2)
+    lines = clock.render("# t", s, achieved_tflops=1000.0)
+    assert any(line.startswith("achieved_tflops: 1000.0") for line in lines)
+    with pytest.raises(ValueError):
+        clock.summarize(rec[3:])

@@ -33,6 +33,8 @@ FA_ACC = {"fp32": 0, "fp16": 1}
 FA_CAUSAL = {"none": 0, "top_left": 1, "bottom_right": 2}
 # 64-bit words per workgroup record of trace mode (fa_fwd_trace).
 TRACE_WORDS = 8
+# Workspace bytes fa_fwd_noalloc's static device array holds (FA_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 class FaProblem(C.Structure):
@@ -75,6 +77,8 @@ SIGNATURES = {
     "fa_fwd_trace": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p,
                                C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64,
                                C.c_void_p]),
+    "fa_fwd_noalloc": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p,
+                                 C.c_void_p, C.c_void_p]),
     "fa_fwd_tile": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "fa_fwd_select": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32)]),
     "fa_kernel_count": (C.c_int, []),

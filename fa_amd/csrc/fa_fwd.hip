@@ -895,8 +895,9 @@ int check_strides(const fa_problem* p, const fa_strides* s, const KeyLayout& lay
 }
 
 // Tiles above 64 KiB of LDS need the per-kernel dynamic-LDS limit raised,
-// once per kernel function and device. The flags are the library's only
-// state; setting one twice (two threads racing on a first call) is harmless.
+// once per kernel function and device. These flags and the per-device
+// scratch addresses of fa_fwd_noalloc are the library's only host state;
+// setting either twice (two threads racing on a first call) is harmless.
 constexpr int kMaxDevices = 64;
 std::atomic<uint8_t> g_lds_ready[kMaxDevices][kNumTiles][2][3];
 
@@ -995,9 +996,50 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
   return FA_OK;
 }
 
+// Device address of this file's scratch array on the current device (set up
+// on the first call per device, with that device current).
+int scratch_address(void** out);
+
+}  // namespace
+
+// Workspace of fa_fwd_noalloc(): one copy per device, held from module load
+// until the process ends. Host code never uses the array's name as an
+// address (on the host it is only a stand-in for the symbol); it asks the
+// runtime for the device address once per device and passes that on.
+static __device__ __align__(256) unsigned char scratch[FA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+std::atomic<void*> g_scratch[kMaxDevices];
+
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FA_ERR_LAUNCH;
+  void* ptr = g_scratch[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return FA_ERR_LAUNCH;
+    g_scratch[dev].store(ptr, std::memory_order_release);
+  }
+  *out = ptr;
+  return FA_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int fa_fwd_noalloc(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
+                   void* stream) {
+  uint64_t need = 0;
+  int rc = fa_fwd_workspace_bytes(p, &need);
+  if (rc) return rc;
+  if (need > FA_NOALLOC_SCRATCH_BYTES) return FA_ERR_SCRATCH;
+  if (!q || !k || !v || !o) return FA_ERR_NULL;
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc) return rc;
+  return launch(p, nullptr, q, k, v, o, Extras{}, ws, FA_NOALLOC_SCRATCH_BYTES, stream);
+}
 
 int fa_fwd_workspace_bytes(const fa_problem* p, uint64_t* bytes) {
   if (!bytes) return FA_ERR_NULL;
@@ -1112,6 +1154,7 @@ const char* fa_strerror(int status) {
     case FA_ERR_CAPTURE: return "capture needs a stats buffer of fa_fwd_capture_count() floats";
     case FA_ERR_CAUSAL: return "unknown causal mode";
     case FA_ERR_TRACE: return "trace needs a buffer of fa_fwd_trace_count() 64-bit words";
+    case FA_ERR_SCRATCH: return "problem needs more workspace than fa_fwd_noalloc's scratch (FA_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown status";
   }
 }

@@ -50,7 +50,8 @@ enum fa_status {
   FA_ERR_LAUNCH = 10,       /* the HIP runtime rejected a launch */
   FA_ERR_CAPTURE = 11,      /* capture stats buffer too small */
   FA_ERR_CAUSAL = 12,       /* unknown causal mode */
-  FA_ERR_TRACE = 13         /* trace buffer too small */
+  FA_ERR_TRACE = 13,        /* trace buffer too small */
+  FA_ERR_SCRATCH = 14       /* fa_fwd_noalloc: workspace need above FA_NOALLOC_SCRATCH_BYTES */
 };
 
 enum fa_acc {
@@ -209,6 +210,26 @@ int fa_kernel_count(void);
 
 /* Static name of tile configuration `kernel` (1..fa_kernel_count()), or NULL. */
 const char* fa_kernel_name(int32_t kernel);
+
+/*
+ * fa_fwd() without a caller workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * workspace (the transposed V and, with a ragged key tail, padded K and V^T)
+ * lives in a static device array of FA_NOALLOC_SCRATCH_BYTES per GPU, which
+ * the library holds from module load until the process ends; problems whose
+ * fa_fwd_workspace_bytes() exceeds it fail with FA_ERR_SCRATCH before any
+ * work is enqueued (64 MiB covers e.g. B * Hkv * Nk = 2 * 131072 keys with no
+ * key tail, the B=2 N=131072 configuration). Nothing is allocated or freed:
+ * the first call on a device looks up that device's array address
+ * (hipGetSymbolAddress) and keeps it. Every call on one GPU shares that
+ * array and each call overwrites what it uses, so calls that overlap on one
+ * GPU (different streams, or threads) race and must be serialised by the
+ * caller; the array's contents on entry do not matter.
+ */
+#define FA_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int fa_fwd_noalloc(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
+                   void* stream);
 
 /* Static message for a status code. */
 const char* fa_strerror(int status);

@@ -232,3 +232,17 @@ def test_strided_validation(lib):
     assert call(k=(256 * 128, -8, 128)) == 2                     # negative stride
     assert call(o=(4 * 256 * 128, 256 * 128, 64)) == 2           # rows overlap
     assert call(k=(0, 0, 1 << 23), v=(0, 0, 128)) == 2           # key rows span >= 2^31 bytes
+
+
+def test_noalloc_rejects_before_touching_the_gpu(lib):
+    # Problems whose workspace exceeds the static scratch (64 MiB) and NULL
+    # tensors are refused on the host.
+    fake = C.c_void_p(4096)
+    big = problem(batch=4, seq_q=256, seq_k=131072)          # 4 * 131072 keys * 256 B = 128 MiB
+    assert lib.fa_fwd_noalloc(C.byref(big), fake, fake, fake, fake, None) == 14
+    assert lib.fa_fwd_noalloc(C.byref(problem(dim=64)), fake, fake, fake, fake, None) == 3
+    assert lib.fa_fwd_noalloc(C.byref(problem()), None, fake, fake, fake, None) == 1
+    assert lib.fa_fwd_noalloc(None, fake, fake, fake, fake, None) == 1
+    # The headline configuration (B=2, Nk=131072, no key tail) fits exactly.
+    rc, size = ws_bytes(lib, problem(batch=2, seq_q=131072, seq_k=131072))
+    assert rc == 0 and size == binding.NOALLOC_SCRATCH_BYTES

@@ -34,7 +34,7 @@ FA_CAUSAL = {"none": 0, "top_left": 1, "bottom_right": 2}
 # 64-bit words per workgroup record of trace mode (fa_fwd_trace).
 TRACE_WORDS = 8
 # Workspace bytes fa_fwd_noalloc's static device array holds (FA_NOALLOC_SCRATCH_BYTES).
-NOALLOC_SCRATCH_BYTES = 64 << 20
+NOALLOC_SCRATCH_BYTES = (64 << 20) + (64 << 10)
 
 
 class FaProblem(C.Structure):

@@ -43,6 +43,7 @@
 #include <stdint.h>
 #include <math.h>
 
+#include <algorithm>
 #include <atomic>
 #include <type_traits>
 
@@ -71,18 +72,18 @@ constexpr float LN2 = 0.6931471805599453f;
 // ran and two clock stamps around its key loop. Both are separate kernels.
 enum KernelMode { MODE_RUN = 0, MODE_CAPTURE = 1, MODE_TRACE = 2 };
 
-// Trace record of one workgroup (64-bit words, record index = blockIdx.x):
-//   0  hardware placement: HW_ID register (wave slot, SIMD, CU, shader array,
-//      shader engine) in bits 0-31, XCC_ID (the accelerator die, one of 8)
-//      in bits 32-35, both read by wave 0
-//   1  s_memrealtime at kernel entry (constant 100 MHz reference clock)
-//   2  s_memrealtime after the key loop (every wave past the final barrier)
-//   3  s_memtime at kernel entry (shader-clock cycles)
-//   4  s_memtime after the key loop
-//   5  blockIdx.x
-//   6  key blocks the workgroup streamed
+// Trace record of one query tile (64-bit words, record index = tile index):
+//   0  hardware placement of the workgroup that ran it: HW_ID register (wave
+//      slot, SIMD, CU, shader array, shader engine) in bits 0-31, XCC_ID (the
+//      accelerator die, one of 8) in bits 32-35, both read by wave 0
+//   1  s_memrealtime when the tile starts (constant 100 MHz reference clock)
+//   2  s_memrealtime after its key loop (every wave past the final barrier)
+//   3  s_memtime when the tile starts (shader-clock cycles)
+//   4  s_memtime after its key loop
+//   5  tile index
+//   6  key blocks the tile streamed
 //   7  keys per block
-// The shader clock the workgroup ran at is (w4 - w3) / (w2 - w1) * 100 MHz.
+// The shader clock the tile ran at is (w4 - w3) / (w2 - w1) * 100 MHz.
 constexpr int TRACE_WORDS = 8;
 
 // Kernel arguments. seq_k is the key length of the K and V^T buffers the
@@ -111,6 +112,8 @@ struct FaArgs {
   float* lse;
   float* stats;
   uint64_t* trace;
+  int* next_tile;      // work-queue counter (workspace), zeroed by the prep kernel
+  int tiles;           // query tiles of the launch: B * Hq * ceil(Nq / 256)
   int heads_q, group, seq_q, seq_k, nk_valid;
   int causal, causal_off;
   float c;
@@ -153,15 +156,17 @@ __device__ __forceinline__ int vt_key_of_slot(int slot) {
 // group's K rows are also copied to kpad[kv][key0 + r] (zero rows past
 // nk_valid), the padded K a masked key tail reads. Grid (nk_pad / 64, B * Hkv),
 // 256 threads; v and k hold nk_valid keys per head with strides vs and ks,
-// vt and kpad are contiguous with nk_pad keys per head.
+// vt and kpad are contiguous with nk_pad keys per head. It also resets the
+// attention kernel's tile counter.
 __global__ void __launch_bounds__(256) fa_prep_kernel(const _Float16* __restrict__ k,
                                                       const _Float16* __restrict__ v,
                                                       _Float16* __restrict__ vt,
                                                       _Float16* __restrict__ kpad, int nk_valid,
                                                       int nk_pad, int heads_kv, Strides ks,
-                                                      Strides vs) {
+                                                      Strides vs, int* __restrict__ next_tile) {
   __shared__ _Float16 tile[VT_GROUP][HD + 8];
   const int tid = threadIdx.x;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) *next_tile = 0;   // the attention kernel's work queue
   const size_t kv = blockIdx.y;
   const int b = (int)(kv / heads_kv), hk = (int)(kv % heads_kv);
   const int key0 = blockIdx.x * VT_GROUP;
@@ -205,10 +210,10 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Trace mode: thread 0 writes the workgroup's record (layout at TRACE_WORDS)
-// with the entry stamps real0/clk0 and stamps taken now.
-__device__ __forceinline__ void trace_record(const FaArgs& args, uint64_t real0, uint64_t clk0,
-                                             int nblk, int bn) {
+// Trace mode: thread 0 writes the tile's record (layout at TRACE_WORDS)
+// with the start stamps real0/clk0 and stamps taken now.
+__device__ __forceinline__ void trace_record(const FaArgs& args, int tile, uint64_t real0,
+                                             uint64_t clk0, int nblk, int bn) {
   const uint64_t real1 = __builtin_amdgcn_s_memrealtime();
   const uint64_t clk1 = __builtin_amdgcn_s_memtime();
   if (threadIdx.x != 0) return;
@@ -216,13 +221,13 @@ __device__ __forceinline__ void trace_record(const FaArgs& args, uint64_t real0,
   // and XCC_ID (id 20), all 32 bits.
   const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
   const uint32_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20) & 15u;
-  uint64_t* rec = args.trace + (size_t)blockIdx.x * TRACE_WORDS;
+  uint64_t* rec = args.trace + (size_t)tile * TRACE_WORDS;
   rec[0] = (uint64_t)hw | ((uint64_t)xcc << 32);
   rec[1] = real0;
   rec[2] = real1;
   rec[3] = clk0;
   rec[4] = clk1;
-  rec[5] = blockIdx.x;
+  rec[5] = (uint64_t)tile;
   rec[6] = (uint64_t)nblk;
   rec[7] = (uint64_t)bn;
 }
@@ -250,7 +255,7 @@ __device__ __forceinline__ void trace_record(const FaArgs& args, uint64_t real0,
 // rescale runs only on the rare blocks where some row of the wave needs it.
 // With TAU = 0 the max tracks every increase (FP16 O must not grow).
 template <bool ACC16, int BN, int NS, int MODE>
-__device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
+__device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
   constexpr bool CAPTURE = MODE == MODE_CAPTURE;
   constexpr bool TRACE = MODE == MODE_TRACE;
   uint64_t real0 = 0, clk0 = 0;
@@ -294,7 +299,12 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   char* kbase = lds;                     // NS K blocks
   char* vbase = lds + NS * KBYTES;       // NS V^T blocks
 
-  const int tid = threadIdx.x;
+  // The thread index passes through an opaque move, so nothing derived from
+  // it is hoisted out of the work-queue loop around this function: values a
+  // tile can recompute in a few instructions would otherwise stay live in
+  // registers across every tile's key loop.
+  int tid;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
   const int lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hf = lane >> 5;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);   // provably wave-uniform
@@ -304,20 +314,20 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
 
   // Query tiles may run past Nq (a ragged last tile): its rows past the end
   // compute on a copy of the last row and store nothing. Without a mask,
-  // consecutive workgroups walk the query tiles of one (batch, head); with the
-  // causal mask, whose tiles differ in work, they walk the heads of one query
-  // tile, the tiles with the most key blocks first, so the short tiles fill
-  // the end of the dispatch.
+  // consecutive tile indices walk the query tiles of one (batch, head); with
+  // the causal mask, whose tiles differ in work, they walk the heads of one
+  // query tile, the tiles with the most key blocks first, so the short tiles
+  // are taken last.
   const int tiles_q = (seq_q + BM - 1) / BM;
-  const int nbh = gridDim.x / tiles_q;
+  const int nbh = args.tiles / tiles_q;
   int bh, qt;
   if (args.causal) {
-    const int r = blockIdx.x / nbh;
-    bh = blockIdx.x - r * nbh;
+    const int r = tile / nbh;
+    bh = tile - r * nbh;
     qt = tiles_q - 1 - r;
   } else {
-    bh = blockIdx.x / tiles_q;
-    qt = blockIdx.x - bh * tiles_q;
+    bh = tile / tiles_q;
+    qt = tile - bh * tiles_q;
   }
   const int b = bh / heads_q, h = bh - b * heads_q;
   const int heads_kv = heads_q / group;
@@ -356,7 +366,7 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
         }
       }
     }
-    if constexpr (TRACE) trace_record(args, real0, clk0, 0, BN);
+    if constexpr (TRACE) trace_record(args, tile, real0, clk0, 0, BN);
     if (!row_ok) return;
     if (args.lse && hf == 0) args.lse[grow] = -INFINITY;
     const h4 zero = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
@@ -451,18 +461,29 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   static_assert(1 + DSTEP * (NIW - 1) < 2 * NQK, "every DMA instruction finds an MFMA slot");
 
   f32x16 acc[4];
-  h2 acc16[4][8];
-  f32x16 part[4];
   f32x16 s[KT];
   h8 p[KS];
-  float m = NEG_BIG, lsum = 0.f, alpha_prev = 1.f;
+  float m = NEG_BIG, lsum = 0.f;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) {
-    acc[dt] = f32x16{};
-    part[dt] = f32x16{};
+  for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x16{};
+  // FP16 accumulator: O is an FP16 value at every packet boundary. The
+  // matrix cores accumulate a packet's PV products (rescaled like the FP32
+  // accumulator when the max moves) on top of it in the FP32 registers, and
+  // at the packet's end the sum is rounded to FP16 in place -- the merge
+  // O16 = fp16(alpha O16 + partial) of the reference's FP16-O kernel, once
+  // per 512 keys, its packet (there: the partial rounded to FP16 first, and
+  // an FP16 alpha). An O beyond the FP16 range becomes inf, as there.
+  constexpr int PACKET = 512 / BN;       // key blocks per packet
+  auto round_acc_fp16 = [&]() {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc16[dt][i] = h2{(_Float16)0.f, (_Float16)0.f};
-  }
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        const h2 t = {(_Float16)acc[dt][i], (_Float16)acc[dt][i + 1]};
+        acc[dt][i] = (float)t[0];
+        acc[dt][i + 1] = (float)t[1];
+      }
+  };
 #pragma unroll
   for (int i = 0; i < KS; ++i) p[i] = h8{};
   const h2 ones = {(_Float16)1.f, (_Float16)1.f};
@@ -495,13 +516,10 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
     for (int i = 0; i < 2 * NQK; ++i) {
       const h8 a = fr[i % PF];
       const int n = i >> 1;
-      // The first product into each S tile (and, for the FP16 accumulator,
-      // each PV partial) starts from a zero accumulator operand instead of
-      // zeroed registers.
+      // The first product into each S tile starts from a zero accumulator
+      // operand instead of zeroed registers.
       if ((i & 1) == 0) {
         s[n % KT] = mfma32(a, qf[n / KT], n < KT ? f32x16{} : s[n % KT]);
-      } else if constexpr (ACC16) {
-        part[n % 4] = mfma32(a, p[n / 4], n < 4 ? f32x16{} : part[n % 4]);
       } else {
         acc[n % 4] = mfma32(a, p[n / 4], acc[n % 4]);
       }
@@ -533,19 +551,13 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   wait_dma(0);
   lds_barrier();
 
-  // VALU step: online softmax of S(j) into P(j) (and, for the FP16
-  // accumulator, the merge of the PV(j-1) partial computed by MFMA step j).
+  // VALU step: online softmax of S(j) into P(j). For the FP16 accumulator,
+  // when block j starts a packet, acc holds the previous packet's PV products
+  // (the last of them added by MFMA step j): it is rounded to FP16 first.
   auto valu_step = [&](int key0, auto masked) {
     if constexpr (ACC16) {
-      const _Float16 a16 = (_Float16)alpha_prev;
-      const h2 a2 = {a16, a16};
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const h2 pv = {(_Float16)part[dt][2 * i], (_Float16)part[dt][2 * i + 1]};
-          acc16[dt][i] = acc16[dt][i] * a2 + pv;
-        }
+      const int j = key0 / BN;
+      if (j > 0 && j % PACKET == 0) round_acc_fp16();
     }
     // Keys past the row's limit (zero padding of a ragged last block, keys
     // beyond the causal diagonal) get MASKED added to their score, so P = 0.
@@ -589,18 +601,13 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
       alpha = __builtin_amdgcn_exp2f((m - mnew) * c);
       m = mnew;
       lsum *= alpha;
-      if constexpr (!ACC16) {
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) acc[dt] *= alpha;
-      }
+      for (int dt = 0; dt < 4; ++dt) acc[dt] *= alpha;
     }
-    alpha_prev = alpha;
     const float mc = m * c;
-    // Row sum in four independent partial sums. The FP32 accumulator sums
-    // the FP16-rounded P the PV products use (one dot per pair); the FP16
-    // accumulator, whose softmax step is the longer of its two, sums the
-    // unrounded FP32 P with two adds (measured 3% faster there, 6% slower
-    // for the FP32 accumulator).
+    // Row sum in four independent partial sums of the FP16-rounded P the PV
+    // products use (one dot per pair), so numerator and denominator use
+    // identical weights.
     float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
@@ -614,8 +621,7 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
           const h2 pr = {(_Float16)p0, (_Float16)p1};
           frag[e] = pr[0];
           frag[e + 1] = pr[1];
-          if constexpr (ACC16) ls[e >> 1] += p0 + p1;
-          else ls[e >> 1] = __builtin_amdgcn_fdot2(pr, ones, ls[e >> 1], false);
+          ls[e >> 1] = __builtin_amdgcn_fdot2(pr, ones, ls[e >> 1], false);
         }
         p[2 * t + g2] = frag;
       }
@@ -695,7 +701,7 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   }
   // No DMA may still be writing this workgroup's LDS when it exits.
   wait_dma(0);
-  if constexpr (TRACE) trace_record(args, real0, clk0, nblk, BN);
+  if constexpr (TRACE) trace_record(args, tile, real0, clk0, nblk, BN);
 
   if constexpr (CAPTURE) {
     // Key blocks past the causal diagonal leave every statistic unchanged.
@@ -711,18 +717,8 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
     }
   }
 
-  if constexpr (ACC16) {
-    // The last block's PV (computed in the final MFMA step) is still pending.
-    const _Float16 a16 = (_Float16)alpha_prev;
-    const h2 a2 = {a16, a16};
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const h2 pv = {(_Float16)part[dt][2 * i], (_Float16)part[dt][2 * i + 1]};
-        acc16[dt][i] = acc16[dt][i] * a2 + pv;
-      }
-  }
+  // FP16 accumulator: the last (possibly partial) packet's merge.
+  if constexpr (ACC16) round_acc_fp16();
 
   // Epilogue: O / l -> FP16 and the row's log-sum-exp
   // ln(l) + scale * m = (log2(l) + c * m) * ln 2, for rows inside Nq. A row
@@ -739,13 +735,73 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
       h4 out;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float x;
-        if constexpr (ACC16) x = (float)acc16[dt][(4 * g + e) >> 1][e & 1];
-        else x = acc[dt][4 * g + e];
-        out[e] = (_Float16)(x * inv);
+        out[e] = (_Float16)(acc[dt][4 * g + e] * inv);
       }
       *reinterpret_cast<h4*>(orow + dt * 32 + 8 * g + 4 * hf) = out;
     }
+  }
+}
+
+// The attention kernel is persistent: a launch has one workgroup per CU (the
+// LDS ring allows no second one), and each workgroup takes query tiles from a
+// shared counter until none are left. The 8 accelerator dies run at clocks
+// that differ by up to ~10% under the board's power limit; with a fixed
+// tile-to-workgroup mapping every die gets the same number of tiles and the
+// launch ends with the slowest one, while from a shared counter the faster
+// dies take more tiles. Every workgroup leaves once the counter passes the
+// tile count, so the grid drains. The counter lives in the workspace and is
+// zeroed by the prep kernel, which runs first on the same stream.
+// Copy of the kernel arguments read from the kernel-argument segment at
+// address `addr` (scalar loads), field by field.
+typedef const FaArgs __attribute__((address_space(4)))* KernargArgs;
+__device__ __forceinline__ Strides load_strides(const Strides __attribute__((address_space(4)))& s) {
+  return Strides{s.b, s.h, s.n};
+}
+__device__ __forceinline__ FaArgs load_args(uint64_t addr) {
+  KernargArgs a = reinterpret_cast<KernargArgs>(addr);
+  FaArgs r;
+  r.q = a->q;
+  r.k = a->k;
+  r.vt = a->vt;
+  r.o = a->o;
+  r.lse = a->lse;
+  r.stats = a->stats;
+  r.trace = a->trace;
+  r.next_tile = a->next_tile;
+  r.tiles = a->tiles;
+  r.heads_q = a->heads_q;
+  r.group = a->group;
+  r.seq_q = a->seq_q;
+  r.seq_k = a->seq_k;
+  r.nk_valid = a->nk_valid;
+  r.causal = a->causal;
+  r.causal_off = a->causal_off;
+  r.c = a->c;
+  r.qs = load_strides(a->qs);
+  r.ks = load_strides(a->ks);
+  r.os = load_strides(a->os);
+  return r;
+}
+
+template <bool ACC16, int BN, int NS, int MODE>
+__device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
+  __shared__ int claimed;
+  for (;;) {
+    if (threadIdx.x == 0) claimed = atomicAdd(args.next_tile, 1);
+    __syncthreads();
+    const int tile = __builtin_amdgcn_readfirstlane(claimed);
+    if (tile >= args.tiles) break;
+    // Each tile reloads the arguments from the kernel-argument segment
+    // through an address the compiler cannot follow across iterations: kept
+    // from one tile to the next, all of them would stay live in scalar
+    // registers across every key loop, and at 256 VGPRs per wave that
+    // pressure spills.
+    uint64_t addr = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
+    asm volatile("" : "+s"(addr));
+    fa_pp_tile<ACC16, BN, NS, MODE>(load_args(addr), tile);
+    // Every wave has read `claimed` (and finished with the LDS ring) before
+    // thread 0 claims the next tile.
+    __syncthreads();
   }
 }
 
@@ -784,6 +840,7 @@ struct TileConfig {
 };
 constexpr int kThreads = 512;     // 8 waves
 constexpr int kRows = 256;        // BM: 8 waves x 32 query rows
+constexpr uint64_t kCounterBytes = 256;
 
 #define FA_TILE(NAME, BN, NS)                                                               \
   TileConfig {                                                                              \
@@ -803,11 +860,10 @@ const TileConfig kTiles[] = {
     FA_TILE("pp_n128_r2", 128, 2),    // 128-key blocks, 2-slot LDS ring
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
-// Automatic choice (fa_problem.kernel == 0), measured fastest at N = 32768
-// and 65536: the 128-key tile for FP32 O; for FP16 O, whose 128-key tile
-// spills registers, the 3-slot 64-key ring.
+// Automatic choice (fa_problem.kernel == 0), measured fastest at N = 65536
+// for both accumulators: the 128-key tile.
 constexpr int kAutoFp32 = 3;
-constexpr int kAutoFp16 = 1;
+constexpr int kAutoFp16 = 3;
 
 int select_tile(const fa_problem* p, const TileConfig** out) {
   int idx = p->kernel;
@@ -826,6 +882,10 @@ struct KeyLayout {
   int64_t nk_pad;
   bool pad_k;
   uint64_t vt_bytes, k_bytes;
+  // Workspace: V^T, then the padded K (ragged key tails only), then the
+  // attention kernel's tile counter in a 256-byte slot of its own.
+  uint64_t counter_offset() const { return vt_bytes + k_bytes; }
+  uint64_t workspace_bytes() const { return vt_bytes + k_bytes + kCounterBytes; }
 };
 
 KeyLayout key_layout(const fa_problem* p, const TileConfig* tile) {
@@ -869,7 +929,7 @@ uint64_t capture_count(const fa_problem* p, const TileConfig* tile, const KeyLay
   return 4ull * (uint64_t)(lay.nk_pad / tile->keys) * (uint64_t)(p->batch * p->heads_q * p->seq_q);
 }
 
-// Workgroups of one attention launch (one per 256 query rows of a (b, h)).
+// Query tiles of one attention launch (one per 256 query rows of a (b, h)).
 uint64_t grid_size(const fa_problem* p) {
   return (uint64_t)(p->batch * p->heads_q) * (uint64_t)((p->seq_q + kRows - 1) / kRows);
 }
@@ -914,6 +974,24 @@ int ensure_lds_limit(const TileConfig* tile, int acc, int mode) {
   return FA_OK;
 }
 
+// Compute units of the current device (the persistent grid's size), looked
+// up once per device.
+std::atomic<int> g_cus[kMaxDevices];
+
+int device_cus(int* cus) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FA_ERR_LAUNCH;
+  int n = g_cus[dev].load(std::memory_order_acquire);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      return FA_ERR_LAUNCH;
+    g_cus[dev].store(n, std::memory_order_release);
+  }
+  *cus = n;
+  return FA_OK;
+}
+
 // Optional outputs of one launch: per-row LSE, capture statistics, trace records.
 struct Extras {
   float* lse = nullptr;
@@ -941,7 +1019,7 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
     vs = strides_of(strides->v);
     os = strides_of(strides->o);
   }
-  if (!workspace || workspace_bytes < lay.vt_bytes + lay.k_bytes) return FA_ERR_WORKSPACE;
+  if (!workspace || workspace_bytes < lay.workspace_bytes()) return FA_ERR_WORKSPACE;
   for (const void* ptr : {q, k, v, (const void*)o, (const void*)workspace, (const void*)ex.lse,
                           (const void*)ex.stats, (const void*)ex.trace})
     if (reinterpret_cast<uintptr_t>(ptr) & 15) return FA_ERR_ALIGN;
@@ -951,10 +1029,14 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
   const int mode = ex.stats ? MODE_CAPTURE : ex.trace ? MODE_TRACE : MODE_RUN;
   rc = ensure_lds_limit(tile, acc, mode);
   if (rc) return rc;
+  int cus = 0;
+  rc = device_cus(&cus);
+  if (rc) return rc;
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   _Float16* vt = static_cast<_Float16*>(workspace);
   _Float16* kpad = lay.pad_k ? vt + lay.vt_bytes / sizeof(_Float16) : nullptr;
+  int* next_tile = reinterpret_cast<int*>(static_cast<char*>(workspace) + lay.counter_offset());
 
   // hipLaunchKernel returns the status of this launch alone; errors left
   // pending by the caller's earlier work are neither read nor cleared.
@@ -962,7 +1044,7 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
     const _Float16* kk = static_cast<const _Float16*>(k);
     const _Float16* vv = static_cast<const _Float16*>(v);
     int nk_valid = (int)p->seq_k, nk_pad = (int)lay.nk_pad, heads_kv = (int)p->heads_kv;
-    void* prep_args[] = {&kk, &vv, &vt, &kpad, &nk_valid, &nk_pad, &heads_kv, &ks, &vs};
+    void* prep_args[] = {&kk, &vv, &vt, &kpad, &nk_valid, &nk_pad, &heads_kv, &ks, &vs, &next_tile};
     const dim3 prep_grid((unsigned)(lay.nk_pad / VT_GROUP), (unsigned)(p->batch * p->heads_kv));
     if (hipLaunchKernel(reinterpret_cast<const void*>(&fa_prep_kernel), prep_grid, dim3(256),
                         prep_args, 0, st) != hipSuccess)
@@ -977,6 +1059,8 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
   args.lse = ex.lse;
   args.stats = ex.stats;
   args.trace = ex.trace;
+  args.next_tile = next_tile;
+  args.tiles = (int)grid_size(p);
   args.heads_q = (int)p->heads_q;
   args.group = (int)(p->heads_q / p->heads_kv);
   args.seq_q = (int)p->seq_q;
@@ -989,9 +1073,11 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
   args.os = os;
   args.ks = lay.pad_k ? contiguous(p->heads_kv, lay.nk_pad) : ks;
   void* attn_args[] = {&args};
-  if (hipLaunchKernel(reinterpret_cast<const void*>(tile->fn[acc][mode]),
-                      dim3((unsigned)grid_size(p)), dim3(kThreads), attn_args, tile->lds,
-                      st) != hipSuccess)
+  // One workgroup per CU (the LDS ring leaves room for no second one), never
+  // more workgroups than tiles.
+  const unsigned grid = (unsigned)std::min<uint64_t>(grid_size(p), (uint64_t)cus);
+  if (hipLaunchKernel(reinterpret_cast<const void*>(tile->fn[acc][mode]), dim3(grid),
+                      dim3(kThreads), attn_args, tile->lds, st) != hipSuccess)
     return FA_ERR_LAUNCH;
   return FA_OK;
 }
@@ -1047,7 +1133,7 @@ int fa_fwd_workspace_bytes(const fa_problem* p, uint64_t* bytes) {
   int rc = validate(p, &tile);
   if (rc) return rc;
   const KeyLayout lay = key_layout(p, tile);
-  *bytes = lay.vt_bytes + lay.k_bytes;
+  *bytes = lay.workspace_bytes();
   return FA_OK;
 }
 

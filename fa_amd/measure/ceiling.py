@@ -121,6 +121,7 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--out")
     ap.add_argument("--command", default="")
+    ap.add_argument("--records", help="save the loop's trace records as <prefix>_mode<m>.npy")
     args = ap.parse_args(argv)
     repo = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     if repo not in sys.path:
@@ -135,6 +136,10 @@ def main(argv=None) -> int:
         print(lines[-1], flush=True)
     for mode, label in ((0, "operands in registers"), (1, "A operand read from LDS")):
         rate, records = mfma_loop(mode)
+        if args.records:
+            import numpy as np
+
+            np.save(f"{args.records}_mode{mode}.npy", records)
         s = clock.summarize(records)
         f = s["mean_mhz_time_weighted"]
         lines.append(f"mfma_loop mode {mode} ({label}): {rate:.1f} TFLOP/s = "

@@ -114,6 +114,7 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--out", help="also write the summary to this file")
     ap.add_argument("--command", default="", help="command line recorded in the summary")
+    ap.add_argument("--records", help="also save the raw trace records (.npy)")
     args = ap.parse_args(argv)
     repo = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     if repo not in sys.path:
@@ -121,6 +122,8 @@ def main(argv=None) -> int:
     from fa_amd.problem.cases import CASES
 
     tflops, records, tflops_trace = run_attention(args.case, args.acc, args.warmup, args.steps)
+    if args.records:
+        np.save(args.records, records)
     s = summarize(records)
     lines = render(f"# running shader clock of hip_fa_{args.acc}acc at c{args.case} "
                    f"{CASES[args.case].name} (trace-mode records)", s, tflops)

@@ -9,9 +9,13 @@ known bytes / counter bytes of the calibration kernel, and the two scaled
 figures are added: ``traffic_bytes_per_launch``. The summary file this writes
 under ``profiles/`` is what ``bench.py`` reports as ``roofline.traffic``.
 
+The algorithmic bytes of a launch, against which the traffic is compared,
+come from the configuration (``--case i``): Q and O (B*Hq*Nq*128 FP16 each)
+plus K and V (B*Hkv*Nk*128 FP16 each), every tensor read or written once.
+
 Usage (on the CPU, after the GPU runs):
   python -m fa_amd.measure.traffic --fetch DIR --write DIR --copy-mib M \\
-      --key "<backend> c<i> <case> tile=<tile>" --command-fetch "..." \\
+      --case 3 --key "<backend> c<i> <case> tile=<tile>" --command-fetch "..." \\
       --command-write "..." --out profiles/<name>_traffic.txt
 """
 
@@ -80,19 +84,30 @@ def summarize(fetch_dir, write_dir, copy_mib, attn_needle="hip_fa_", copy_needle
     }
 
 
+def algorithmic_bytes(case):
+    """Bytes a launch must move at least: Q, K, V read and O written once (FP16)."""
+    q_o = case.batch * case.heads_q * case.seq_len * case.dim * 2
+    k_v = case.batch * case.heads_kv * case.seq_len * case.dim * 2
+    return 2 * q_o + 2 * k_v
+
+
 def main(argv=None):
     p = argparse.ArgumentParser(description="HBM bytes per launch from FETCH_SIZE/WRITE_SIZE runs")
     p.add_argument("--fetch", required=True)
     p.add_argument("--write", required=True)
     p.add_argument("--copy-mib", type=int, required=True)
     p.add_argument("--key", required=True)
-    p.add_argument("--algorithmic-bytes", type=int, default=0)
+    p.add_argument("--case", type=int, required=True,
+                   help="configuration index c0..c4 (its Q+K+V+O bytes are the algorithmic bytes)")
     p.add_argument("--command-fetch", default="")
     p.add_argument("--command-write", default="")
     p.add_argument("--out", required=True)
     args = p.parse_args(argv)
     s = summarize(args.fetch, args.write, args.copy_mib)
     total = int(round(s["fetch_bytes"] + s["write_bytes"]))
+    from fa_amd.problem.cases import CASES
+
+    algo = algorithmic_bytes(CASES[args.case])
     lines = [
         "# HBM traffic per launch (rocprofv3 FETCH_SIZE and WRITE_SIZE, separate passes)",
         f"key: {args.key}",
@@ -109,9 +124,8 @@ def main(argv=None):
         f"write_bytes_per_launch: {s['write_bytes']:.0f}",
         f"traffic_bytes_per_launch: {total}",
     ]
-    if args.algorithmic_bytes:
-        lines.append(f"algorithmic_bytes_per_launch: {args.algorithmic_bytes} "
-                     f"(traffic / algorithmic = {total / args.algorithmic_bytes:.3f})")
+    lines.append(f"algorithmic_bytes_per_launch: {algo} (Q + K + V + O of c{args.case}; "
+                 f"traffic / algorithmic = {total / algo:.3f})")
     os.makedirs(os.path.dirname(os.path.abspath(args.out)), exist_ok=True)
     with open(args.out, "w", encoding="utf-8") as f:
         f.write("\n".join(lines) + "\n")

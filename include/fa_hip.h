@@ -56,9 +56,13 @@ enum fa_status {
 
 enum fa_acc {
   FA_ACC_FP32 = 0,          /* O accumulated in FP32 registers across all keys */
-  FA_ACC_FP16 = 1           /* per-block PV rounded to FP16, O accumulated in FP16 */
+  FA_ACC_FP16 = 1           /* O rounded to FP16 after every 512 keys (the reference's packet) */
 };
-/* Range of the FP16 accumulator: O is accumulated unnormalised, as
+/* FP16 accumulator: the matrix cores add each 512-key packet's PV products
+ * (FP32) to O, and O is rounded to FP16 at the end of every packet and after
+ * the last key -- the reference FP16-O kernel's per-packet merge
+ * O16 = fp16(alpha O16 + partial). The row max m is exact (no lazy raise).
+ * Range: O is accumulated unnormalised, as
  * sum_j 2^(s_j c - m c) v_j over the keys seen so far, with m the running
  * row max, so every weight is <= 1 but the sum is not. Once that sum leaves
  * the FP16 range (|.| > 65504, e.g. a long row of nearly equal scores whose
@@ -91,7 +95,8 @@ typedef struct fa_problem {
 /*
  * Bytes of device workspace fa_fwd() needs for problem *p (the key-permuted
  * transposed copy of v; with a ragged key tail, zero-padded copies of k and
- * v^T to a whole key block of the selected tile). Replaces phase 1 of the
+ * v^T to a whole key block of the selected tile; 256 bytes for the counter
+ * the kernel's workgroups take query tiles from). Replaces phase 1 of the
  * reference's operator call,
  * aclnn<Op>GetWorkspaceSize (backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/
  * binding.py:21-24,74-75), whose host tiling sizes the scratch buffer
@@ -219,15 +224,15 @@ const char* fa_kernel_name(int32_t kernel);
  * lives in a static device array of FA_NOALLOC_SCRATCH_BYTES per GPU, which
  * the library holds from module load until the process ends; problems whose
  * fa_fwd_workspace_bytes() exceeds it fail with FA_ERR_SCRATCH before any
- * work is enqueued (64 MiB covers e.g. B * Hkv * Nk = 2 * 131072 keys with no
- * key tail, the B=2 N=131072 configuration). Nothing is allocated or freed:
+ * work is enqueued (64 MiB + 64 KiB covers e.g. B * Hkv * Nk = 2 * 131072
+ * keys with no key tail, the B=2 N=131072 configuration). Nothing is allocated or freed:
  * the first call on a device looks up that device's array address
  * (hipGetSymbolAddress) and keeps it. Every call on one GPU shares that
  * array and each call overwrites what it uses, so calls that overlap on one
  * GPU (different streams, or threads) race and must be serialised by the
  * caller; the array's contents on entry do not matter.
  */
-#define FA_NOALLOC_SCRATCH_BYTES (64ull << 20)
+#define FA_NOALLOC_SCRATCH_BYTES ((64ull << 20) + (64ull << 10))
 int fa_fwd_noalloc(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
                    void* stream);
 

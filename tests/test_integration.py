@@ -81,7 +81,7 @@ def test_problem_fields_and_workspace_for_every_configuration(hip_fa, index):
     assert (p.acc, p.kernel, p.causal) == (hip_fa.ACC, 0, 0)
     size = C.c_uint64()
     assert hip_fa._library().fa_fwd_workspace_bytes(C.byref(p), C.byref(size)) == 0
-    assert size.value == case.batch * case.heads_kv * case.seq_len * 128 * 2
+    assert size.value == case.batch * case.heads_kv * case.seq_len * 128 * 2 + 256
 
 
 def test_adapt_on_host_tensors_and_its_errors(hip_fa):

@@ -50,10 +50,11 @@ def lib(library_path):
 
 
 def test_workspace_size(lib):
+    # V^T, plus 256 bytes for the work-queue counter.
     rc, size = ws_bytes(lib, problem(batch=2, heads_kv=1, seq_k=131072))
-    assert rc == 0 and size == 2 * 1 * 131072 * 128 * 2
+    assert rc == 0 and size == 2 * 1 * 131072 * 128 * 2 + 256
     rc, size = ws_bytes(lib, problem(heads_q=8, heads_kv=4, seq_q=512, seq_k=1024))
-    assert rc == 0 and size == 4 * 1024 * 128 * 2
+    assert rc == 0 and size == 4 * 1024 * 128 * 2 + 256
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -76,12 +77,12 @@ def test_ragged_tails_and_workspace(lib):
         rc, size = ws_bytes(lib, problem(seq_q=nq, seq_k=nk))
         assert rc == 0, (nq, nk)
         pad = -(-nk // 128) * 128
-        assert size == 2 * pad * 128 * 2, (nq, nk, size)
+        assert size == 2 * pad * 128 * 2 + 256, (nq, nk, size)
     rc, size = ws_bytes(lib, problem(seq_q=300, seq_k=4096))
-    assert rc == 0 and size == 4096 * 128 * 2          # no key tail: V^T only
+    assert rc == 0 and size == 4096 * 128 * 2 + 256    # no key tail: V^T only
     # A 64-key tile pads to whole 64-key blocks.
     rc, size = ws_bytes(lib, problem(seq_q=300, seq_k=1000, kernel=1))
-    assert rc == 0 and size == 2 * 1024 * 128 * 2
+    assert rc == 0 and size == 2 * 1024 * 128 * 2 + 256
     for kernel in range(lib.fa_kernel_count() + 1):      # every tile masks tails
         rows, keys = C.c_int32(), C.c_int32()
         assert lib.fa_fwd_tile(C.byref(problem(kernel=kernel)), C.byref(rows), C.byref(keys)) == 0
@@ -118,8 +119,8 @@ def test_capture_count_and_rejections(lib):
     count, block = C.c_uint64(), C.c_int32()
     assert lib.fa_fwd_capture_count(C.byref(prob), C.byref(count), C.byref(block)) == 0
     assert block.value == 128 and count.value == 4 * 8 * 12 * 300
-    prob16 = problem(seq_q=300, seq_k=1000, acc=1)   # FP16 default tile: 64-key blocks
-    assert lib.fa_fwd_capture_count(C.byref(prob16), C.byref(count), C.byref(block)) == 0
+    prob64 = problem(seq_q=300, seq_k=1000, acc=1, kernel=1)   # a 64-key tile
+    assert lib.fa_fwd_capture_count(C.byref(prob64), C.byref(count), C.byref(block)) == 0
     assert block.value == 64 and count.value == 4 * 16 * 12 * 300
     assert lib.fa_fwd_capture_count(C.byref(prob), None, C.byref(block)) == 1
     # Launch-time checks happen on the host, before any GPU work.
@@ -185,13 +186,13 @@ def test_kernel_table(lib):
 
 
 def test_automatic_choice(lib):
-    # kernel = 0: the 128-key tile for FP32 O, the 3-slot 64-key ring for FP16 O.
+    # kernel = 0: the 128-key tile for both accumulators.
     sel = C.c_int32()
     for seq in (4096, 131072, 1000):
-        assert lib.fa_fwd_select(C.byref(problem(seq_q=seq, seq_k=seq)), C.byref(sel)) == 0
-        assert lib.fa_kernel_name(sel.value) == b"pp_n128_r2"
-        assert lib.fa_fwd_select(C.byref(problem(seq_q=seq, seq_k=seq, acc=1)), C.byref(sel)) == 0
-        assert lib.fa_kernel_name(sel.value) == b"pp_n64_r3"
+        for acc in (0, 1):
+            prob = problem(seq_q=seq, seq_k=seq, acc=acc)
+            assert lib.fa_fwd_select(C.byref(prob), C.byref(sel)) == 0
+            assert lib.fa_kernel_name(sel.value) == b"pp_n128_r2"
 
 
 def test_operator_validation_without_gpu(library_path):
@@ -243,6 +244,6 @@ def test_noalloc_rejects_before_touching_the_gpu(lib):
     assert lib.fa_fwd_noalloc(C.byref(problem(dim=64)), fake, fake, fake, fake, None) == 3
     assert lib.fa_fwd_noalloc(C.byref(problem()), None, fake, fake, fake, None) == 1
     assert lib.fa_fwd_noalloc(None, fake, fake, fake, fake, None) == 1
-    # The headline configuration (B=2, Nk=131072, no key tail) fits exactly.
+    # The headline configuration (B=2, Nk=131072, no key tail) fits.
     rc, size = ws_bytes(lib, problem(batch=2, seq_q=131072, seq_k=131072))
-    assert rc == 0 and size == binding.NOALLOC_SCRATCH_BYTES
+    assert rc == 0 and size <= binding.NOALLOC_SCRATCH_BYTES

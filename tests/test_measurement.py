@@ -125,3 +125,14 @@ def test_clock_summary_from_trace_records():
     assert any(line.startswith("achieved_tflops: 1000.0") for line in lines)
     with pytest.raises(ValueError):
         clock.summarize(rec[3:])
+
+
+def test_algorithmic_bytes_of_every_configuration():
+    from fa_amd.problem.cases import CASES
+
+    # Q + K + V + O, FP16: c3 is 2*12*131072*128*2 (Q) twice plus 2*1*131072*128*2 (K) twice.
+    assert traffic.algorithmic_bytes(CASES[3]) == 1_744_830_464
+    assert traffic.algorithmic_bytes(CASES[0]) == 2 * (12 + 1) * 4096 * 256
+    for case in CASES:
+        assert traffic.algorithmic_bytes(case) == 2 * case.batch * (case.heads_q + case.heads_kv) \
+            * case.seq_len * case.dim * 2

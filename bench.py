@@ -221,7 +221,7 @@ def main(argv=None):
                           "p10_mhz": round(s["p10_mhz"], 1), "p90_mhz": round(s["p90_mhz"], 1),
                           "mfma_roof_at_clock": round(clock.roof_at(f), 1),
                           "frac_at_clock": round(tflops / clock.roof_at(f), 4),
-                          "source": "fa_fwd_trace records (s_memtime / s_memrealtime per workgroup)"}
+                          "source": "fa_fwd_trace records (s_memtime / s_memrealtime per query tile)"}
             del traced
         sustained = ceiling.measure(gemm_reps=10)
         sustained["frac_of_gemm"] = round(tflops / sustained["gemm_best_tflops"], 4)

@@ -31,7 +31,7 @@ FA_ACC = {"fp32": 0, "fp16": 1}
 # scaled_dot_product_attention(is_causal=True)) or bottom-right
 # (j <= i + Nk - Nq).
 FA_CAUSAL = {"none": 0, "top_left": 1, "bottom_right": 2}
-# 64-bit words per workgroup record of trace mode (fa_fwd_trace).
+# 64-bit words per query-tile record of trace mode (fa_fwd_trace).
 TRACE_WORDS = 8
 # Workspace bytes fa_fwd_noalloc's static device array holds (FA_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = (64 << 20) + (64 << 10)
@@ -104,8 +104,8 @@ class AttentionConfig:
     statistics per key block (the reference config's ``capture`` flag,
     ``backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/backend.py:27``), the
     attention mask (``FA_CAUSAL``; a row that sees no key gets O = 0 and
-    lse = -inf), and trace mode, which records per workgroup where it ran
-    and its clock stamps (the reference kernel's ``trace`` output)."""
+    lse = -inf), and trace mode, which records per 256-row query tile where
+    it ran and its clock stamps (the reference kernel's ``trace`` output)."""
     acc: str = "fp32"
     kernel: int = 0
     capture: bool = False
@@ -241,7 +241,7 @@ class Operator:
         keys, each row's running max m (natural-log units), running sum l
         relative to m, rescale factor alpha and block sum z relative to m.
         With ``config.trace`` it fills ``self.last["trace"]``, int64
-        [workgroups, 8]: the per-workgroup records of ``fa_fwd_trace``."""
+        [tiles, 8]: the per-query-tile records of ``fa_fwd_trace``."""
         import torch
 
         self.validate(q, k, v)

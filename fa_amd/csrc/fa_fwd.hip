@@ -68,7 +68,7 @@ constexpr double LOG2E = 1.4426950408889634;
 constexpr float LN2 = 0.6931471805599453f;
 
 // Kernel instantiation modes. Capture records the online-softmax statistics
-// of every row after every key block; trace records, per workgroup, where it
+// of every row after every key block; trace records, per query tile, where it
 // ran and two clock stamps around its key loop. Both are separate kernels.
 enum KernelMode { MODE_RUN = 0, MODE_CAPTURE = 1, MODE_TRACE = 2 };
 
@@ -95,7 +95,7 @@ constexpr int TRACE_WORDS = 8;
 // holding the running max m (natural-log units, scale * score), the running
 // sum l relative to m, the rescale factor alpha applied at that block, and
 // the block's own row sum z relative to m. trace, in trace mode, receives
-// one record of TRACE_WORDS 64-bit words per workgroup (see trace_record). c is the softmax scale times
+// one record of TRACE_WORDS 64-bit words per query tile (see trace_record). c is the softmax scale times
 // log2(e). With causal set, query row i sees keys j <= i + causal_off only
 // (causal_off = 0 aligns the mask top-left, Nk - Nq bottom-right); a row that
 // sees no key gets O = 0 and lse = -inf. qs, ks and os are the element

@@ -1,10 +1,11 @@
-"""Running shader clock of a kernel, from the per-workgroup trace records.
+"""Running shader clock of a kernel, from its trace records.
 
-Both the attention kernel's trace mode (``fa_fwd_trace``) and the MFMA
-ceiling kernel write one record of 8 uint64 words per workgroup: words 1/2
-are ``s_memrealtime`` (a constant 100 MHz reference clock) at entry and after
-the main loop, words 3/4 ``s_memtime`` (shader-clock cycles) at the same
-points. ``summarize`` turns the records into the clock each workgroup ran at,
+The attention kernel's trace mode (``fa_fwd_trace``) writes one record of 8
+uint64 words per 256-row query tile, the MFMA ceiling kernel one per
+workgroup: words 1/2 are ``s_memrealtime`` (a constant 100 MHz reference
+clock) at the start and after the main loop, words 3/4 ``s_memtime``
+(shader-clock cycles) at the same points. ``summarize`` turns the records
+into the clock each tile or workgroup ran at,
 ``(w4 - w3) / (w2 - w1) * 100 MHz``, and its spread over the launch and over
 the 8 accelerator dies (XCC_ID, word 0 bits 32-35, attention kernel only).
 
@@ -29,7 +30,7 @@ PEAK_CLOCK_MHZ = 2400.0
 
 
 def clocks_mhz(records) -> np.ndarray:
-    """Per-workgroup shader clock (MHz) of records with a nonzero time span."""
+    """Shader clock (MHz) of each record with a nonzero time span."""
     r = np.asarray(records, dtype=np.int64).reshape(-1, 8)
     real = (r[:, 2] - r[:, 1]).astype(np.float64)
     cyc = (r[:, 4] - r[:, 3]).astype(np.float64)
@@ -48,7 +49,7 @@ def summarize(records) -> dict:
                if np.any((xcc == x) & (real > 0))}
     weights = real[real > 0].astype(np.float64)
     return {
-        "workgroups": int(r.shape[0]),
+        "records": int(r.shape[0]),
         "median_mhz": float(np.median(mhz)),
         "mean_mhz_time_weighted": float(np.sum(mhz * weights) / np.sum(weights)),
         "p10_mhz": float(np.percentile(mhz, 10)),
@@ -57,7 +58,7 @@ def summarize(records) -> dict:
         "max_mhz": float(mhz.max()),
         "per_xcc_median_mhz": per_xcc,
         "span_ms": float((r[:, 2].max() - r[:, 1].min()) / (REF_CLOCK_MHZ * 1e3)),
-        "workgroup_ms_median": float(np.median(real) / (REF_CLOCK_MHZ * 1e3)),
+        "record_ms_median": float(np.median(real) / (REF_CLOCK_MHZ * 1e3)),
     }
 
 
@@ -68,12 +69,12 @@ def roof_at(mhz: float) -> float:
 
 def render(title, s, achieved_tflops=None) -> list:
     lines = [title,
-             f"workgroups: {s['workgroups']}",
+             f"records: {s['records']}",
              f"clock_mhz: median {s['median_mhz']:.0f}, time-weighted mean "
              f"{s['mean_mhz_time_weighted']:.0f}, p10 {s['p10_mhz']:.0f}, p90 {s['p90_mhz']:.0f}, "
              f"min {s['min_mhz']:.0f}, max {s['max_mhz']:.0f}",
              f"span_ms: {s['span_ms']:.3f} (first entry to last loop end), "
-             f"per-workgroup median {s['workgroup_ms_median']:.3f}"]
+             f"per-record median {s['record_ms_median']:.3f}"]
     if s["per_xcc_median_mhz"]:
         lines.append("per_xcc_median_mhz: " + ", ".join(
             f"{x}: {v:.0f}" for x, v in s["per_xcc_median_mhz"].items()))

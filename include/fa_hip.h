@@ -171,20 +171,24 @@ int fa_fwd_capture(const fa_problem* p, const void* q, const void* k, const void
 
 /*
  * Trace mode: fa_fwd() that also writes one record of 8 uint64 words per
- * workgroup of the attention kernel into trace (16-byte aligned, at least
+ * 256-row query tile of the attention kernel into trace (16-byte aligned, at least
  * fa_fwd_trace_count() words), the counterpart of the reference kernel's
  * per-core trace output, which records each core's id and its start and end
  * system-counter values (K32/panel_kernel.h:222-225,340-342; buffer
- * binding.py:44). Record of workgroup w, words 8w .. 8w+7:
- *   0  HW_ID register (bits 0-31) and XCC_ID (bits 32-35) of wave 0
- *   1  s_memrealtime at entry (100 MHz reference clock)
- *   2  s_memrealtime after the key loop
- *   3  s_memtime at entry (shader clock cycles)
- *   4  s_memtime after the key loop
- *   5  workgroup index w
+ * binding.py:44). Tile w covers the 256 query rows 256r .. 256r+255 of one
+ * (b, h): w = (b*Hq + h) * ceil(Nq/256) + r without a mask, and
+ * w = (ceil(Nq/256) - 1 - r) * B*Hq + b*Hq + h with a causal mask (longest
+ * tiles first). Record of tile w, words 8w .. 8w+7:
+ *   0  HW_ID register (bits 0-31) and XCC_ID (bits 32-35) of wave 0 of the
+ *      workgroup that ran the tile
+ *   1  s_memrealtime when the tile starts (100 MHz reference clock)
+ *   2  s_memrealtime after its key loop
+ *   3  s_memtime when the tile starts (shader clock cycles)
+ *   4  s_memtime after its key loop
+ *   5  tile index w
  *   6  key blocks streamed
  *   7  keys per block
- * so the shader clock the workgroup ran at is (w4 - w3) / (w2 - w1) * 100
+ * so the shader clock the tile ran at is (w4 - w3) / (w2 - w1) * 100
  * MHz. The trace kernel is a separate instantiation of the same tile (the
  * production kernels carry no stamps); its O is the production kernel's.
  */

@@ -1,7 +1,7 @@
 """Trace mode and the MFMA ceiling kernel on the GPU.
 
 Trace mode (fa_fwd_trace) is a separate instantiation of the production tile:
-its O must equal the production kernel's bit for bit, and every workgroup must
+its O must equal the production kernel's bit for bit, and every query tile must
 leave a well-formed record (its index, the key blocks it streamed, the block
 size, monotonic clock stamps, a plausible clock and accelerator die). The
 ceiling kernel must run, keep its sums finite, and report a plausible clock.

@@ -133,7 +133,7 @@ def test_capture_count_and_rejections(lib):
 
 
 def test_trace_count_and_rejections(lib):
-    # One 8-word record per workgroup: B * Hq * ceil(Nq / 256) workgroups.
+    # One 8-word record per query tile: B * Hq * ceil(Nq / 256) tiles.
     prob = problem(batch=2, seq_q=300, seq_k=1000)
     count = C.c_uint64()
     assert lib.fa_fwd_trace_count(C.byref(prob), C.byref(count)) == 0

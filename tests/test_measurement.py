@@ -107,7 +107,7 @@ def test_clock_summary_from_trace_records():
 
     from fa_amd.measure import clock
 
-    # Two workgroups on die 1 at 1500 MHz, one on die 3 at 2000 MHz, one empty record.
+    # Two records on die 1 at 1500 MHz, one on die 3 at 2000 MHz, one empty record.
     rec = np.zeros((4, 8), dtype=np.int64)
     rec[0] = [(1 << 32) | 5, 1000, 2000, 10, 10 + 15_000, 0, 8, 128]     # 1000 ticks = 10 us
     rec[1] = [(1 << 32) | 6, 1000, 3000, 50, 50 + 30_000, 1, 8, 128]
@@ -115,7 +115,7 @@ def test_clock_summary_from_trace_records():
     rec[3] = [0, 7, 7, 0, 0, 3, 0, 128]
     assert np.allclose(clock.clocks_mhz(rec), [1500, 1500, 2000])
     s = clock.summarize(rec)
-    assert s["workgroups"] == 4 and s["median_mhz"] == 1500
+    assert s["records"] == 4 and s["median_mhz"] == 1500
     assert s["per_xcc_median_mhz"] == {1: 1500.0, 3: 2000.0}
     # Weighted by each record's span: (1500*1000 + 1500*2000 + 2000*1000) / 4000.
     assert s["mean_mhz_time_weighted"] == pytest.approx(1625.0)

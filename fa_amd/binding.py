@@ -77,6 +77,8 @@ SIGNATURES = {
     "fa_fwd_trace": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p,
                                C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64,
                                C.c_void_p]),
+    "fa_fwd_sync": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p,
+                              C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
     "fa_fwd_noalloc": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p,
                                  C.c_void_p, C.c_void_p]),
     "fa_fwd_tile": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
@@ -104,13 +106,17 @@ class AttentionConfig:
     statistics per key block (the reference config's ``capture`` flag,
     ``backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/backend.py:27``), the
     attention mask (``FA_CAUSAL``; a row that sees no key gets O = 0 and
-    lse = -inf), and trace mode, which records per 256-row query tile where
-    it ran and its clock stamps (the reference kernel's ``trace`` output)."""
+    lse = -inf), trace mode, which records per 256-row query tile where
+    it ran and its clock stamps (the reference kernel's ``trace`` output),
+    and the synchronous debug mode (``fa_fwd_sync``: poisoned staging
+    buffers, no load/compute overlap; the reference's ``SYNCHRONOUS`` build
+    flag), whose output must equal the production kernel's bit for bit."""
     acc: str = "fp32"
     kernel: int = 0
     capture: bool = False
     causal: str = "none"
     trace: bool = False
+    sync: bool = False
 
     def __post_init__(self):
         if self.acc not in FA_ACC:
@@ -123,8 +129,10 @@ class AttentionConfig:
             raise ValueError(f"unknown causal mode {self.causal!r}")
         if not isinstance(self.trace, bool):
             raise ValueError("trace must be a bool")
-        if self.trace and self.capture:
-            raise ValueError("capture and trace are separate kernels; pick one")
+        if not isinstance(self.sync, bool):
+            raise ValueError("sync must be a bool")
+        if self.trace + self.capture + self.sync > 1:
+            raise ValueError("capture, trace and sync are separate kernels; pick one")
 
 
 def make_problem(q_shape, k_shape, scale, config):
@@ -257,8 +265,8 @@ class Operator:
         stats, block = self.stats_for(q, k, prob) if capture else (None, 0)
         trace = self.trace_for(q, k, prob) if self.config.trace else None
         strided = not all(t.is_contiguous() for t in (q, k, v))
-        if strided and (capture or trace is not None):
-            raise ValueError("capture and trace modes need contiguous Q/K/V")
+        if strided and (capture or trace is not None or self.config.sync):
+            raise ValueError("capture, trace and sync modes need contiguous Q/K/V")
         with torch.cuda.device(q.device):
             need = max(size.value, 16)
             if self.workspace is None or self.workspace.device != q.device \
@@ -281,6 +289,9 @@ class Operator:
             elif trace is not None:
                 status = self.lib.fa_fwd_trace(C.byref(prob), *common, trace.data_ptr(),
                                                trace.numel(), *tail)
+            elif self.config.sync:
+                status = self.lib.fa_fwd_sync(C.byref(prob), *common,
+                                              lse.data_ptr() if lse is not None else None, *tail)
             elif return_lse:
                 status = self.lib.fa_fwd_lse(C.byref(prob), *common, lse.data_ptr(), *tail)
             else:

@@ -69,8 +69,15 @@ constexpr float LN2 = 0.6931471805599453f;
 
 // Kernel instantiation modes. Capture records the online-softmax statistics
 // of every row after every key block; trace records, per query tile, where it
-// ran and two clock stamps around its key loop. Both are separate kernels.
-enum KernelMode { MODE_RUN = 0, MODE_CAPTURE = 1, MODE_TRACE = 2 };
+// ran and two clock stamps around its key loop. Sync is the synchronous
+// debug mode: every tile's LDS ring starts poisoned with FP16 NaN and each
+// phase's loads complete before the phase ends, so a read of LDS no load has
+// filled, or a race between the loads and the operand reads, changes the
+// output. All three are separate kernels.
+enum KernelMode { MODE_RUN = 0, MODE_CAPTURE = 1, MODE_TRACE = 2, MODE_SYNC = 3 };
+constexpr int kModes = 4;
+// FP16 quiet NaN in both halves of a 32-bit word: the poison of sync mode.
+constexpr uint32_t NAN16X2 = 0x7e007e00u;
 
 // Trace record of one query tile (64-bit words, record index = tile index):
 //   0  hardware placement of the workgroup that ran it: HW_ID register (wave
@@ -210,6 +217,13 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Sync mode: fill n16 16-byte words at p with FP16 NaN (grid-stride).
+__global__ void __launch_bounds__(256) fa_poison_kernel(u32x4* p, uint64_t n16) {
+  const u32x4 nan = {NAN16X2, NAN16X2, NAN16X2, NAN16X2};
+  for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * 256)
+    p[i] = nan;
+}
+
 // Trace mode: thread 0 writes the tile's record (layout at TRACE_WORDS)
 // with the start stamps real0/clk0 and stamps taken now.
 __device__ __forceinline__ void trace_record(const FaArgs& args, int tile, uint64_t real0,
@@ -258,6 +272,7 @@ template <bool ACC16, int BN, int NS, int MODE>
 __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
   constexpr bool CAPTURE = MODE == MODE_CAPTURE;
   constexpr bool TRACE = MODE == MODE_TRACE;
+  constexpr bool SYNC = MODE == MODE_SYNC;
   uint64_t real0 = 0, clk0 = 0;
   if constexpr (TRACE) {
     real0 = __builtin_amdgcn_s_memrealtime();
@@ -495,23 +510,31 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
 
   // MFMA step for block j: S^T(j) = K(j) Q^T and O^T += V^T(j-1) P^T(j-1),
   // QK and PV MFMAs interleaved, operands prefetched PF MFMAs ahead.
-  auto mfma_step = [&](const char* kb, const char* vb, bool with_dma, int dkb, int dks, int dvb,
-                       int dvs) {
-    // QK op n covers S tile n % KT at k-step n / KT, so consecutive QK ops
-    // alternate accumulators; with PV ops in between, no accumulator is
-    // reused within four MFMAs and dependent MFMAs never wait on each other.
-    auto ld = [&](int i) -> h8 {
-      const int n = i >> 1;
-      if ((i & 1) == 0) {
-        const int t = n % KT, kk = n / KT;
-        return *reinterpret_cast<const h8*>(kb + k_lane + t * 32 * KROW + kk * 32);
-      }
-      const int dt = n % 4, ks = n / 4;
-      return *reinterpret_cast<const h8*>(vb + v_lane + dt * 32 * VROW + ks * 32);
-    };
-    h8 fr[PF];
+  // Operand i of a step: QK op n = i / 2 (even i) covers S tile n % KT at
+  // k-step n / KT, so consecutive QK ops alternate accumulators; with PV ops
+  // in between, no accumulator is reused within four MFMAs and dependent
+  // MFMAs never wait on each other.
+  auto ld = [&](const char* kb, const char* vb, int i) -> h8 {
+    const int n = i >> 1;
+    if ((i & 1) == 0) {
+      const int t = n % KT, kk = n / KT;
+      return *reinterpret_cast<const h8*>(kb + k_lane + t * 32 * KROW + kk * 32);
+    }
+    const int dt = n % 4, ks = n / 4;
+    return *reinterpret_cast<const h8*>(vb + v_lane + dt * 32 * VROW + ks * 32);
+  };
+  // The step's first PF operands. A group-1 wave reads them at the end of
+  // the VALU step before its MFMA step (its blocks were published one phase
+  // earlier), so its MFMA step starts without waiting for LDS; a group-0
+  // step reads them itself.
+  h8 fr[PF];
+  auto preload = [&](const char* kb, const char* vb) {
 #pragma unroll
-    for (int i = 0; i < PF; ++i) fr[i] = ld(i);
+    for (int i = 0; i < PF; ++i) fr[i] = ld(kb, vb, i);
+  };
+  auto mfma_step = [&](const char* kb, const char* vb, bool with_dma, int dkb, int dks, int dvb,
+                       int dvs, auto preloaded) {
+    if constexpr (!decltype(preloaded)::value) preload(kb, vb);
 #pragma unroll
     for (int i = 0; i < 2 * NQK; ++i) {
       const h8 a = fr[i % PF];
@@ -523,7 +546,7 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
       } else {
         acc[n % 4] = mfma32(a, p[n / 4], acc[n % 4]);
       }
-      if (i + PF < 2 * NQK) fr[i % PF] = ld(i + PF);
+      if (i + PF < 2 * NQK) fr[i % PF] = ld(kb, vb, i + PF);
       if (i >= 1 && (i - 1) % DSTEP == 0 && (i - 1) / DSTEP < NIW) {
         if (with_dma) dma_one((i - 1) / DSTEP, dkb, dks, dvb, dvs);
       }
@@ -532,6 +555,13 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
     }
   };
 
+  if constexpr (SYNC) {
+    // Poison the whole ring (every K and V^T slot, row pads included), so an
+    // operand read of LDS that no load of this tile has written is a NaN.
+    for (int i = tid; i < NS * (KBYTES + VBYTES) / 16; i += NT)
+      reinterpret_cast<u32x4*>(lds)[i] = u32x4{NAN16X2, NAN16X2, NAN16X2, NAN16X2};
+    lds_barrier();
+  }
   // V^T slot NS-1 (read as "V(-1)" by the first MFMA step) starts as zeros:
   // the first step multiplies it by P = 0.
   for (int i = tid; i < VBYTES / 16; i += NT)
@@ -663,15 +693,16 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
   // (the ragged tail, the causal diagonal), which always applies the
   // per-element mask. A wave-uniform test inside one loop measured 1-3%
   // slower than no test, even when never taken.
-  const std::integral_constant<bool, false> unmasked;
-  const std::integral_constant<bool, true> masked;
+  const std::integral_constant<bool, false> unmasked, loads;
+  const std::integral_constant<bool, true> masked, preloaded;
   const int nfull = klim_w + 1 < BN ? 0 : min(nblk, (klim_w + 1) / BN);
   int sl = 0;
   if (grp == 0) {
     auto pair = [&](int j, auto mask) {
       const int sp = prev(sl);
       mfma_step(kslot(sl), vslot(sp), true, min(j + NS - 1, last), sp, min(j + NS - 2, last),
-                prev(sp));             // phase 2j: pair j starts
+                prev(sp), loads);      // phase 2j: pair j starts
+      if constexpr (SYNC) wait_dma(0);   // sync mode: this phase's loads land in it
       lds_barrier();
       valu_step(j * BN, mask);       // phase 2j + 1
       wait_dma(keep);                // K(j+1), V(j) have landed
@@ -681,22 +712,26 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
     int j = 0;
     for (; j < nfull; ++j) pair(j, unmasked);
     for (; j < nblk; ++j) pair(j, masked);
-    mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0);   // phase 2 nblk: PV(nblk - 1)
+    mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0, loads);   // phase 2 nblk: PV(nblk - 1)
     lds_barrier();
     lds_barrier();                           // phase 2 nblk + 1: idle
   } else {
-    lds_barrier();                   // phase 0: this group idles
+    preload(kslot(0), vslot(NS - 1));  // phase 0: this group idles
+    lds_barrier();
     auto pair = [&](int j, auto mask) {
-      mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0);   // phase 2j + 1
+      mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0, preloaded);   // phase 2j + 1
       lds_barrier();
       valu_step(j * BN, mask);       // phase 2j + 2
+      // K(j+1) and V(j), the next step's blocks, were published at this
+      // phase's barrier, and no load writes their slots before pair j + 2.
+      preload(kslot(next(sl)), vslot(sl));
       lds_barrier();
       sl = next(sl);
     };
     int j = 0;
     for (; j < nfull; ++j) pair(j, unmasked);
     for (; j < nblk; ++j) pair(j, masked);
-    mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0);   // phase 2 nblk + 1: PV(nblk - 1)
+    mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0, preloaded);   // phase 2 nblk + 1: PV(nblk - 1)
     lds_barrier();
   }
   // No DMA may still be writing this workgroup's LDS when it exits.
@@ -812,9 +847,9 @@ constexpr int pp_lds_bytes(int bn, int ns) { return ns * (bn * (HD * 2 + 16) + H
 // Device entry points, one per accumulation variant. Their names contain the
 // backend names of the two accumulation variants, which is how a profile
 // attributes kernel time to a backend. Template parameters: BN keys per
-// block, NS slots in the LDS ring, MODE (production, capture or trace; each
-// mode is a separate kernel, so the production kernels carry none of the
-// debug code). 8 waves of 64 lanes, two per SIMD.
+// block, NS slots in the LDS ring, MODE (production, capture, trace or sync;
+// each mode is a separate kernel, so the production kernels carry none of
+// the debug code). 8 waves of 64 lanes, two per SIMD.
 template <int BN, int NS, int MODE>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 hip_fa_fp32acc_kernel(FaArgs args) {
@@ -836,7 +871,7 @@ struct TileConfig {
   const char* name;
   int keys;        // BN
   int lds;         // dynamic LDS bytes per workgroup
-  attn_fn fn[2][3];   // [acc][mode]
+  attn_fn fn[2][kModes];   // [acc][mode]
 };
 constexpr int kThreads = 512;     // 8 waves
 constexpr int kRows = 256;        // BM: 8 waves x 32 query rows
@@ -846,14 +881,14 @@ constexpr uint64_t kCounterBytes = 256;
   TileConfig {                                                                              \
     NAME, BN, pp_lds_bytes(BN, NS), {                                                       \
       {&hip_fa_fp32acc_kernel<BN, NS, MODE_RUN>, &hip_fa_fp32acc_kernel<BN, NS, MODE_CAPTURE>, \
-       &hip_fa_fp32acc_kernel<BN, NS, MODE_TRACE>},                                         \
+       &hip_fa_fp32acc_kernel<BN, NS, MODE_TRACE>, &hip_fa_fp32acc_kernel<BN, NS, MODE_SYNC>}, \
       {&hip_fa_fp16acc_kernel<BN, NS, MODE_RUN>, &hip_fa_fp16acc_kernel<BN, NS, MODE_CAPTURE>, \
-       &hip_fa_fp16acc_kernel<BN, NS, MODE_TRACE>}                                          \
+       &hip_fa_fp16acc_kernel<BN, NS, MODE_TRACE>, &hip_fa_fp16acc_kernel<BN, NS, MODE_SYNC>}  \
     }                                                                                       \
   }
 
 // Every tile masks ragged query and key tails, applies causal masks and has
-// the capture and trace modes.
+// the capture, trace and sync modes.
 const TileConfig kTiles[] = {
     FA_TILE("pp_n64_r3", 64, 3),      // 64-key blocks, 3-slot LDS ring
     FA_TILE("pp_n64_r4", 64, 4),      // 64-key blocks, 4-slot LDS ring
@@ -959,7 +994,7 @@ int check_strides(const fa_problem* p, const fa_strides* s, const KeyLayout& lay
 // scratch addresses of fa_fwd_noalloc are the library's only host state;
 // setting either twice (two threads racing on a first call) is harmless.
 constexpr int kMaxDevices = 64;
-std::atomic<uint8_t> g_lds_ready[kMaxDevices][kNumTiles][2][3];
+std::atomic<uint8_t> g_lds_ready[kMaxDevices][kNumTiles][2][kModes];
 
 int ensure_lds_limit(const TileConfig* tile, int acc, int mode) {
   if (tile->lds <= 65536) return FA_OK;
@@ -992,13 +1027,15 @@ int device_cus(int* cus) {
   return FA_OK;
 }
 
-// Optional outputs of one launch: per-row LSE, capture statistics, trace records.
+// Optional outputs of one launch (per-row LSE, capture statistics, trace
+// records) and the synchronous debug mode.
 struct Extras {
   float* lse = nullptr;
   float* stats = nullptr;
   uint64_t stats_count = 0;
   uint64_t* trace = nullptr;
   uint64_t trace_count = 0;
+  bool sync = false;
 };
 
 int launch(const fa_problem* p, const fa_strides* strides, const void* q, const void* k,
@@ -1026,7 +1063,7 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
   if (ex.stats && ex.stats_count < capture_count(p, tile, lay)) return FA_ERR_CAPTURE;
   if (ex.trace && ex.trace_count < grid_size(p) * TRACE_WORDS) return FA_ERR_TRACE;
   const int acc = p->acc == FA_ACC_FP16 ? 1 : 0;
-  const int mode = ex.stats ? MODE_CAPTURE : ex.trace ? MODE_TRACE : MODE_RUN;
+  const int mode = ex.stats ? MODE_CAPTURE : ex.trace ? MODE_TRACE : ex.sync ? MODE_SYNC : MODE_RUN;
   rc = ensure_lds_limit(tile, acc, mode);
   if (rc) return rc;
   int cus = 0;
@@ -1040,6 +1077,17 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
 
   // hipLaunchKernel returns the status of this launch alone; errors left
   // pending by the caller's earlier work are neither read nor cleared.
+  if (mode == MODE_SYNC) {
+    // Sync mode: the workspace (V^T, padded K) starts as FP16 NaN, so a read
+    // of any element the prep kernel does not write reaches the output.
+    u32x4* ws = static_cast<u32x4*>(workspace);
+    uint64_t n16 = lay.counter_offset() / 16;
+    void* poison_args[] = {&ws, &n16};
+    const unsigned blocks = (unsigned)std::min<uint64_t>((n16 + 255) / 256, 4096);
+    if (n16 && hipLaunchKernel(reinterpret_cast<const void*>(&fa_poison_kernel), dim3(blocks),
+                               dim3(256), poison_args, 0, st) != hipSuccess)
+      return FA_ERR_LAUNCH;
+  }
   {
     const _Float16* kk = static_cast<const _Float16*>(k);
     const _Float16* vv = static_cast<const _Float16*>(v);
@@ -1214,6 +1262,14 @@ int fa_fwd_trace(const fa_problem* p, const void* q, const void* k, const void* 
   Extras ex;
   ex.trace = trace;
   ex.trace_count = trace_count;
+  return launch(p, nullptr, q, k, v, o, ex, workspace, workspace_bytes, stream);
+}
+
+int fa_fwd_sync(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
+                float* lse, void* workspace, uint64_t workspace_bytes, void* stream) {
+  Extras ex;
+  ex.lse = lse;
+  ex.sync = true;
   return launch(p, nullptr, q, k, v, o, ex, workspace, workspace_bytes, stream);
 }
 

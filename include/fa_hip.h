@@ -18,9 +18,10 @@
  *     otherwise; fa_strerror() names the code;
  *   - nothing here allocates device memory or aborts: the caller owns q, k,
  *     v, o and the workspace, and calls on different streams with different
- *     workspaces are independent. The only library state is a per-device,
- *     per-kernel flag recording that the kernel's dynamic-LDS limit has been
- *     raised (set on first use);
+ *     workspaces are independent. The only library state is, per device, a
+ *     flag per kernel recording that its dynamic-LDS limit has been raised,
+ *     the CU count, and the address of fa_fwd_noalloc()'s static scratch
+ *     array (each set on first use);
  *   - fa_fwd() is asynchronous on the given stream (a hipStream_t passed as
  *     void*, NULL for the default stream).
  *
@@ -196,6 +197,27 @@ int fa_fwd_trace_count(const fa_problem* p, uint64_t* count);
 int fa_fwd_trace(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
                  uint64_t* trace, uint64_t trace_count, void* workspace, uint64_t workspace_bytes,
                  void* stream);
+
+/*
+ * Synchronous debug mode: fa_fwd_lse() (lse may be NULL) through a separate
+ * instantiation of the same tile that removes the overlap of loads and
+ * compute and poisons every buffer the kernels stage through: the workspace
+ * (V^T, padded K) is filled with FP16 NaN before the prep kernel rewrites
+ * it, each query tile fills its whole LDS ring (row pads included) with NaN
+ * before its first load, and the loads of each phase complete before that
+ * phase ends instead of one phase later. A read of staging memory that no
+ * load or prep write filled, or a race between the loads and the operand
+ * reads, then changes the output (NaN, or a difference from fa_fwd()); a
+ * correct build gives fa_fwd()'s output and lse bit for bit. The
+ * counterpart of the reference's SYNCHRONOUS build flag, which adds pipe
+ * barriers between stages and writes a poison value into layout gaps
+ * (cce_fa_nqkq_nz_resident_v13_q768_pool_i4_p128/project/op_kernel/
+ * online_softmax.h:10,60-63; cce_fa_nk_nz_vector_fp32_v5_sumpack/project/
+ * op_kernel/cce_fp16_reduce.h:33-42). Slower than fa_fwd(): for debugging.
+ * Same workspace as fa_fwd().
+ */
+int fa_fwd_sync(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
+                float* lse, void* workspace, uint64_t workspace_bytes, void* stream);
 
 /*
  * Query-row and key granularity fa_fwd() needs for *p: Nq must be a

@@ -151,6 +151,21 @@ def test_trace_count_and_rejections(lib):
         binding.AttentionConfig(trace=True, capture=True)
 
 
+def test_sync_mode_rejections(lib):
+    # fa_fwd_sync validates like fa_fwd_lse before anything is launched.
+    prob = problem(batch=2, seq_q=300, seq_k=1000)
+    p = C.c_void_p(4096)
+    _, size = ws_bytes(lib, prob)
+    assert lib.fa_fwd_sync(C.byref(prob), None, p, p, p, None, p, size, None) == 1
+    assert lib.fa_fwd_sync(C.byref(prob), p, p, p, p, None, p, size - 1, None) == 6
+    assert lib.fa_fwd_sync(C.byref(prob), p, p, p, p, C.c_void_p(4100), p, size, None) == 5
+    assert lib.fa_fwd_sync(C.byref(problem(dim=64)), p, p, p, p, None, p, size, None) == 3
+    assert binding.AttentionConfig(sync=True).sync
+    for bad in ({"sync": True, "trace": True}, {"sync": True, "capture": True}, {"sync": 1}):
+        with pytest.raises(ValueError):
+            binding.AttentionConfig(**bad)
+
+
 def test_fwd_rejects_before_launch(lib):
     prob = problem()
     # NULL tensors, missing workspace and misaligned pointers fail on the host.

@@ -255,14 +255,15 @@ __device__ __forceinline__ void trace_record(const FaArgs& args, int tile, uint6
 // softmax (the FA3 ping-pong schedule, here across the two waves of a SIMD).
 //
 // LDS holds a ring of NS K blocks and NS V^T blocks (NS >= 2). Phase pair t
-// (phases 2t, 2t+1) reads K(t) and V(t-1). During its MFMA step of pair t,
-// group 0 issues the direct-to-LDS loads (buffer_load_dwordx4 ... lds, 1 KiB
-// per wave instruction) of K(t+NS-1) and V(t+NS-2) into the ring slots pair t-1
-// finished with, one load every few MFMAs so the vector-memory issue never
-// stalls the wave for long; the VALU steps carry no load work. Group 0 waits
-// for its pair t+2-NS loads at the end of pair t, before the barrier that
-// opens pair t+1, so every load has NS-1 phase pairs minus part of a phase
-// to land and no VGPR or LDS write instruction is spent on staging.
+// (phases 2t, 2t+1) reads K(t) and V(t-1). In phase 2t the direct-to-LDS
+// loads (buffer_load_dwordx4 ... lds, 1 KiB per wave instruction) of
+// K(t+NS-1) and V(t+NS-2) go out into the ring slots pair t-1 finished with:
+// from group 1's VALU step (FP32 accumulator), or from group 0's MFMA step,
+// one load every few MFMAs so the vector-memory issue never stalls the wave
+// for long (FP16 accumulator). The issuing group waits for its pair t+2-NS
+// loads before the barrier that opens pair t+1, so every load has NS-1
+// phase pairs minus part of a phase to land and no VGPR or LDS write
+// instruction is spent on staging.
 //
 // The running max is raised lazily (TAU, in log2 units): a row keeps its max
 // until a block exceeds it by more than TAU, so P <= 2^TAU and the O/l
@@ -697,15 +698,25 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
   const std::integral_constant<bool, true> masked, preloaded;
   const int nfull = klim_w + 1 < BN ? 0 : min(nblk, (klim_w + 1) / BN);
   int sl = 0;
+  // Who issues the loads. Pair t's loads, K(t+NS-1) -> slot (t-1) % NS and
+  // V(t+NS-2) -> slot (t-2) % NS, go out in phase 2t (pair 0's in phase 0),
+  // either from group 0's MFMA step or from group 1's VALU step, which runs
+  // in the same phase and has time to spare while the FP32 softmax runs: the
+  // MFMA steps then carry no load issue (+0.5% at c2/c3). The FP16
+  // accumulator's VALU step also rounds O every fourth block and has no time
+  // to spare (there the move measured 1.7% slower), so its loads stay with
+  // group 0. The wave that issues a pair's loads also waits for them, at the
+  // end of the phase before the loaded blocks are read.
+  constexpr bool LOADS_IN_VALU = !ACC16;
   if (grp == 0) {
     auto pair = [&](int j, auto mask) {
       const int sp = prev(sl);
-      mfma_step(kslot(sl), vslot(sp), true, min(j + NS - 1, last), sp, min(j + NS - 2, last),
-                prev(sp), loads);      // phase 2j: pair j starts
-      if constexpr (SYNC) wait_dma(0);   // sync mode: this phase's loads land in it
+      mfma_step(kslot(sl), vslot(sp), !LOADS_IN_VALU, min(j + NS - 1, last), sp,
+                min(j + NS - 2, last), prev(sp), loads);   // phase 2j: pair j starts
+      if constexpr (SYNC && !LOADS_IN_VALU) wait_dma(0);   // sync mode: loads land in their phase
       lds_barrier();
       valu_step(j * BN, mask);       // phase 2j + 1
-      wait_dma(keep);                // K(j+1), V(j) have landed
+      if constexpr (!LOADS_IN_VALU) wait_dma(keep);        // K(j+1), V(j) have landed
       lds_barrier();
       sl = next(sl);
     };
@@ -716,11 +727,20 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
     lds_barrier();
     lds_barrier();                           // phase 2 nblk + 1: idle
   } else {
+    if constexpr (LOADS_IN_VALU) {       // phase 0: pair 0's loads
+      issue(min(NS - 1, last), NS - 1, min(NS - 2, last), NS - 2);
+      if constexpr (SYNC) wait_dma(0);
+    }
     preload(kslot(0), vslot(NS - 1));  // phase 0: this group idles
     lds_barrier();
     auto pair = [&](int j, auto mask) {
       mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0, preloaded);   // phase 2j + 1
+      if constexpr (LOADS_IN_VALU) wait_dma(keep);         // K(j+1), V(j) have landed
       lds_barrier();
+      if constexpr (LOADS_IN_VALU) {     // pair j + 1's loads
+        issue(min(j + NS, last), sl, min(j + NS - 1, last), prev(sl));
+        if constexpr (SYNC) wait_dma(0);
+      }
       valu_step(j * BN, mask);       // phase 2j + 2
       // K(j+1) and V(j), the next step's blocks, were published at this
       // phase's barrier, and no load writes their slots before pair j + 2.

@@ -24,7 +24,8 @@ pairs the mask leaves, 4*B*Hq*D*pairs.
 ``clock`` (HIP backends) is the shader clock the attention kernel ran at,
 from one trace-mode forward after the timed region, with the MFMA roof at
 that clock; ``sustained`` is the board's sustained dense FP16 matrix rate
-measured in the same process (torch FP16 GEMMs and an MFMA-only loop,
+measured in the same process (torch FP16 GEMMs, an MFMA-only loop and the
+same loop with LDS operands and the softmax's VALU mix,
 ``fa_amd.measure.ceiling``), with ``value`` as a fraction of each.
 
 ``--copy-mib M`` additionally runs ``--copy-reps`` plain device-to-device
@@ -226,6 +227,8 @@ def main(argv=None):
         sustained = ceiling.measure(gemm_reps=10)
         sustained["frac_of_gemm"] = round(tflops / sustained["gemm_best_tflops"], 4)
         sustained["frac_of_mfma_loop"] = round(tflops / sustained["mfma_loop_best_tflops"], 4)
+        sustained["frac_of_softmax_mix_loop"] = round(
+            tflops / sustained["softmax_mix_loop_tflops"], 4)
 
     workload_key = f"{args.backend} c{args.case} {case.name} tile={tile_name}"
     if args.causal != "none":

@@ -10,6 +10,13 @@
 //   MODE 1  each MFMA's A operand is first read from LDS (one ds_read_b128
 //           per lane, four reads in flight), as a GEMM or the attention
 //           kernel's MFMA step feeds the pipe.
+//   MODE 2  MODE 1 plus, after every MFMA, the attention kernel's softmax
+//           work per MFMA: one v_exp_f32 and three other FP32 VALU
+//           operations (the forward issues about 240 VALU instructions, 64
+//           of them exponentials, per 64 MFMAs), on registers independent
+//           of the MFMAs, so nothing waits on a result: the rate of a
+//           pipeline with the forward's operand traffic and instruction mix
+//           but without its data dependencies and barriers.
 //
 // Operands are FP16 values supplied by the caller (random normal data, so the
 // datapath toggles as it does on real inputs). Every wave keeps four
@@ -53,6 +60,11 @@ fa_mfma_ceiling_kernel(const _Float16* __restrict__ operands, float* __restrict_
     a[j] = reinterpret_cast<const h8*>(operands)[(j * 64 + lane) & (kOperandHalves / 8 - 1)];
     b[j] = reinterpret_cast<const h8*>(operands)[(256 + j * 64 + lane) & (kOperandHalves / 8 - 1)];
   }
+  // MODE 2's VALU operands: bounded values (2^w / 2 maps [-1, 1] into
+  // [0.25, 1]; the fused multiply-adds contract towards zero).
+  float w[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) w[j] = (float)operands[(lane * 16 + j) & (kOperandHalves - 1)] * 0.01f;
   __syncthreads();
   f32x16 acc[4] = {};
   // LDS operand address of MFMA n of an iteration: 16 B per lane, 1 KiB per
@@ -71,6 +83,11 @@ fa_mfma_ceiling_kernel(const _Float16* __restrict__ operands, float* __restrict_
         const h8 x = fr[n & 3];
         if (n + 4 < kMfmaPerIter) fr[n & 3] = *reinterpret_cast<const h8*>(base + (n + 4) * 1024);
         acc[n & 3] = mfma32(x, b[n & 3], acc[n & 3]);
+        if constexpr (MODE == 2) {
+          w[n] = __builtin_amdgcn_exp2f(w[n]) * 0.5f;
+          w[(n + 5) & 15] = __builtin_fmaf(w[(n + 5) & 15], 0.999f, -0.001f);
+          w[(n + 11) & 15] = __builtin_fmaf(w[(n + 11) & 15], 0.999f, -0.001f);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -80,6 +97,10 @@ fa_mfma_ceiling_kernel(const _Float16* __restrict__ operands, float* __restrict_
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) sum += acc[j][r];
+  if constexpr (MODE == 2) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sum += w[j];
+  }
   out[(size_t)blockIdx.x * kThreads + tid] = sum;
   if (trace) {
     const uint64_t real1 = __builtin_amdgcn_s_memrealtime();
@@ -107,20 +128,21 @@ uint64_t fa_ceiling_flops_per_workgroup(int iters) {
   return (uint64_t)(kThreads / 64) * (uint64_t)iters * kMfmaPerIter * 32 * 32 * 16 * 2;
 }
 
-// Launch the ceiling kernel: mode 0 (register operands) or 1 (LDS-fed A
-// operand); operands = 8192 FP16 values (16-byte aligned), out = workgroups
+// Launch the ceiling kernel: mode 0 (register operands), 1 (LDS-fed A
+// operand) or 2 (LDS-fed A operand and the softmax's VALU mix); operands = 8192 FP16 values (16-byte aligned), out = workgroups
 // x 512 floats, trace = workgroups x 8 words or NULL. Returns 0, or 1 for
 // bad arguments, 2 when the launch is rejected.
 int fa_ceiling_mfma(int mode, int workgroups, int iters, const void* operands, float* out,
                     uint64_t* trace, void* stream) {
-  if (mode < 0 || mode > 1 || workgroups <= 0 || iters <= 0 || !operands || !out) return 1;
+  if (mode < 0 || mode > 2 || workgroups <= 0 || iters <= 0 || !operands || !out) return 1;
   if ((reinterpret_cast<uintptr_t>(operands) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(trace)) & 15)
     return 1;
   const _Float16* ops = static_cast<const _Float16*>(operands);
   void* args[] = {&ops, &out, &trace, &iters};
-  const void* fn = mode == 0 ? reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<0>)
-                             : reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<1>);
+  const void* fn = mode == 0   ? reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<0>)
+                   : mode == 1 ? reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<1>)
+                               : reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<2>);
   return hipLaunchKernel(fn, dim3((unsigned)workgroups), dim3(kThreads), args, 0,
                          static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : 2;
 }

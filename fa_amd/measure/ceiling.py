@@ -6,8 +6,12 @@ current stream after warmup launches:
 * ``mfma_loop`` -- ``libfa_ceiling.so``: every SIMD of every CU issuing
   nothing but ``v_mfma_f32_32x32x16_f16`` (the attention kernel's matrix
   instruction) from two waves, in the attention kernel's launch shape, with
-  random FP16 operands either in registers (mode 0) or with each A operand
-  read from LDS first (mode 1). Its trace records give the clock it ran at.
+  random FP16 operands either in registers (mode 0), with each A operand
+  read from LDS first (mode 1), or with that LDS traffic plus the attention
+  softmax's VALU instruction mix beside every MFMA (mode 2: one exponential
+  and three other FP32 operations, independent of the MFMAs -- the forward's
+  work without its dependencies and barriers). Its trace records give the
+  clock it ran at.
 * ``gemm`` -- torch's FP16 matrix product (hipBLASLt) on large square and
   rectangular shapes, the rate a tuned vendor GEMM reaches.
 
@@ -28,6 +32,8 @@ import os
 import sys
 
 GEMM_SHAPES = ((8192, 8192, 8192), (8192, 8192, 16384), (16384, 16384, 8192))
+# MFMA loop modes of libfa_ceiling.so and their labels in measure()'s result.
+MODES = ((0, "registers"), (1, "lds_operand"), (2, "lds_operand_softmax_valu"))
 
 
 def _library():
@@ -107,13 +113,14 @@ def measure(gemm_reps=20, loop_iters=16384):
     out = {"gemm_tflops": {}, "mfma_loop": {}}
     for shape, rate in gemm(reps=gemm_reps).items():
         out["gemm_tflops"]["x".join(map(str, shape))] = round(rate, 1)
-    for mode, label in ((0, "registers"), (1, "lds_operand")):
+    for mode, label in MODES:
         rate, records = mfma_loop(mode, iters=loop_iters)
         s = clock.summarize(records)
         out["mfma_loop"][label] = {"tflops": round(rate, 1),
                                    "clock_mhz": round(s["mean_mhz_time_weighted"], 0)}
     out["gemm_best_tflops"] = max(out["gemm_tflops"].values())
     out["mfma_loop_best_tflops"] = max(v["tflops"] for v in out["mfma_loop"].values())
+    out["softmax_mix_loop_tflops"] = out["mfma_loop"]["lds_operand_softmax_valu"]["tflops"]
     return out
 
 
@@ -134,7 +141,8 @@ def main(argv=None) -> int:
         lines.append(f"gemm_fp16 {shape[0]}x{shape[1]}x{shape[2]} (torch.matmul, hipBLASLt): "
                      f"{rate:.1f} TFLOP/s = {rate / clock.PEAK_TFLOPS:.3f} of nominal")
         print(lines[-1], flush=True)
-    for mode, label in ((0, "operands in registers"), (1, "A operand read from LDS")):
+    for mode, label in ((0, "operands in registers"), (1, "A operand read from LDS"),
+                        (2, "A operand from LDS + the softmax's VALU mix")):
         rate, records = mfma_loop(mode)
         if args.records:
             import numpy as np

@@ -62,12 +62,15 @@ def test_trace_records_and_identical_output(library_path, acc, nq, nk, causal):
 def test_ceiling_kernel_runs_and_reports_a_clock():
     from fa_amd.measure import ceiling, clock
 
-    say("case MFMA ceiling kernel, both modes, 256 workgroups")
+    say("case MFMA ceiling kernel, every mode, 256 workgroups")
     lib = ceiling._library()
-    assert lib.fa_ceiling_mfma(2, 1, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
+    # Host-side rejections (nothing is launched): unknown mode, no
+    # workgroups, misaligned operands.
+    assert lib.fa_ceiling_mfma(3, 1, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
+    assert lib.fa_ceiling_mfma(-1, 1, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
     assert lib.fa_ceiling_mfma(0, 0, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
     assert lib.fa_ceiling_mfma(0, 1, 1, C.c_void_p(24), C.c_void_p(16), None, None) == 1
-    for mode in (0, 1):
+    for mode, _ in ceiling.MODES:
         rate, records = ceiling.mfma_loop(mode, workgroups=256, iters=256, reps=1, warmup=1)
         s = clock.summarize(records)
         say(f"  mode {mode}: {rate:.1f} TFLOP/s at {s['median_mhz']:.0f} MHz")

@@ -17,6 +17,9 @@
 //           of the MFMAs, so nothing waits on a result: the rate of a
 //           pipeline with the forward's operand traffic and instruction mix
 //           but without its data dependencies and barriers.
+//   MODE 3  each A operand read from LDS feeds two MFMAs (with different B
+//           operands): the LDS traffic a wave with 64 query rows would
+//           have, half of the attention kernel's.
 //
 // Operands are FP16 values supplied by the caller (random normal data, so the
 // datapath toggles as it does on real inputs). Every wave keeps four
@@ -74,6 +77,18 @@ fa_mfma_ceiling_kernel(const _Float16* __restrict__ operands, float* __restrict_
     if constexpr (MODE == 0) {
 #pragma unroll
       for (int n = 0; n < kMfmaPerIter; ++n) acc[n & 3] = mfma32(a[n >> 2], b[n & 3], acc[n & 3]);
+    } else if constexpr (MODE == 3) {
+      h8 fr[4];
+#pragma unroll
+      for (int f = 0; f < 4; ++f) fr[f] = *reinterpret_cast<const h8*>(base + f * 1024);
+#pragma unroll
+      for (int f = 0; f < kMfmaPerIter / 2; ++f) {
+        const h8 x = fr[f & 3];
+        if (f + 4 < kMfmaPerIter / 2) fr[f & 3] = *reinterpret_cast<const h8*>(base + (f + 4) * 1024);
+        acc[(2 * f) & 3] = mfma32(x, b[0], acc[(2 * f) & 3]);
+        acc[(2 * f + 1) & 3] = mfma32(x, b[1], acc[(2 * f + 1) & 3]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     } else {
       h8 fr[4];
 #pragma unroll
@@ -129,20 +144,23 @@ uint64_t fa_ceiling_flops_per_workgroup(int iters) {
 }
 
 // Launch the ceiling kernel: mode 0 (register operands), 1 (LDS-fed A
-// operand) or 2 (LDS-fed A operand and the softmax's VALU mix); operands = 8192 FP16 values (16-byte aligned), out = workgroups
+// operand), 2 (LDS-fed A operand and the softmax's VALU mix) or 3 (one LDS
+// read per two MFMAs); operands = 8192 FP16 values (16-byte aligned), out = workgroups
 // x 512 floats, trace = workgroups x 8 words or NULL. Returns 0, or 1 for
 // bad arguments, 2 when the launch is rejected.
 int fa_ceiling_mfma(int mode, int workgroups, int iters, const void* operands, float* out,
                     uint64_t* trace, void* stream) {
-  if (mode < 0 || mode > 2 || workgroups <= 0 || iters <= 0 || !operands || !out) return 1;
+  if (mode < 0 || mode > 3 || workgroups <= 0 || iters <= 0 || !operands || !out) return 1;
   if ((reinterpret_cast<uintptr_t>(operands) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(trace)) & 15)
     return 1;
   const _Float16* ops = static_cast<const _Float16*>(operands);
   void* args[] = {&ops, &out, &trace, &iters};
-  const void* fn = mode == 0   ? reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<0>)
-                   : mode == 1 ? reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<1>)
-                               : reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<2>);
+  const void* fns[] = {reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<0>),
+                       reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<1>),
+                       reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<2>),
+                       reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<3>)};
+  const void* fn = fns[mode];
   return hipLaunchKernel(fn, dim3((unsigned)workgroups), dim3(kThreads), args, 0,
                          static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : 2;
 }

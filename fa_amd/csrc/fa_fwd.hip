@@ -475,6 +475,7 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
   // MFMA index after which DMA instruction m is issued inside an MFMA step.
   constexpr int DSTEP = (2 * NQK - 8) / NIW > 0 ? (2 * NQK - 8) / NIW : 1;
   static_assert(1 + DSTEP * (NIW - 1) < 2 * NQK, "every DMA instruction finds an MFMA slot");
+  static_assert(NIW <= 8 * KT, "every DMA instruction finds an exponential pair of a VALU step");
 
   f32x16 acc[4];
   f32x16 s[KT];
@@ -585,7 +586,9 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
   // VALU step: online softmax of S(j) into P(j). For the FP16 accumulator,
   // when block j starts a packet, acc holds the previous packet's PV products
   // (the last of them added by MFMA step j): it is rounded to FP16 first.
-  auto valu_step = [&](int key0, auto masked) {
+  // at(i) runs before the exponentials of score pair i (0 <= i < 8 KT), the
+  // points at which a step that issues loads spreads them.
+  auto valu_step = [&](int key0, auto masked, auto&& at) {
     if constexpr (ACC16) {
       const int j = key0 / BN;
       if (j > 0 && j % PACKET == 0) round_acc_fp16();
@@ -647,6 +650,7 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
         h8 frag;
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
+          at((2 * t + g2) * 4 + e / 2);
           const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * g2 + e], c, -mc));
           const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * g2 + e + 1], c, -mc));
           const h2 pr = {(_Float16)p0, (_Float16)p1};
@@ -715,7 +719,7 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
                 min(j + NS - 2, last), prev(sp), loads);   // phase 2j: pair j starts
       if constexpr (SYNC && !LOADS_IN_VALU) wait_dma(0);   // sync mode: loads land in their phase
       lds_barrier();
-      valu_step(j * BN, mask);       // phase 2j + 1
+      valu_step(j * BN, mask, [](int) {});   // phase 2j + 1
       if constexpr (!LOADS_IN_VALU) wait_dma(keep);        // K(j+1), V(j) have landed
       lds_barrier();
       sl = next(sl);
@@ -737,11 +741,22 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
       mfma_step(kslot(sl), vslot(prev(sl)), false, 0, 0, 0, 0, preloaded);   // phase 2j + 1
       if constexpr (LOADS_IN_VALU) wait_dma(keep);         // K(j+1), V(j) have landed
       lds_barrier();
-      if constexpr (LOADS_IN_VALU) {     // pair j + 1's loads
-        issue(min(j + NS, last), sl, min(j + NS - 1, last), prev(sl));
-        if constexpr (SYNC) wait_dma(0);
-      }
-      valu_step(j * BN, mask);       // phase 2j + 2
+      // Pair j + 1's loads, K(j+NS) -> slot sl and V(j+NS-1) -> prev(sl),
+      // spread over the step's exponentials (in a burst at its start they
+      // measured slower and fetched 4x the bytes from beyond L2).
+      const int kb = min(j + NS, last), ks = sl, vb = min(j + NS - 1, last), vs = prev(sl);
+      valu_step(j * BN, mask, [&](int i) {
+        if constexpr (LOADS_IN_VALU) {
+#pragma unroll
+          for (int mi = 0; mi < NIW; ++mi)
+            if (mi * (8 * KT) / NIW == i) {
+              __builtin_amdgcn_sched_barrier(0);
+              dma_one(mi, kb, ks, vb, vs);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+      });                            // phase 2j + 2
+      if constexpr (LOADS_IN_VALU && SYNC) wait_dma(0);
       // K(j+1) and V(j), the next step's blocks, were published at this
       // phase's barrier, and no load writes their slots before pair j + 2.
       preload(kslot(next(sl)), vslot(sl));

@@ -3,16 +3,17 @@
 //
 // Work decomposition (reference: task = (batch*head, query block), KV head
 // = head / group, backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/project/
-// op_kernel/panel_kernel.h:264-274): one workgroup owns BM query rows of one
-// (batch, head) (BM = 256: the ping-pong body's 8 waves x 32 rows, or the
-// plain body's NW waves x SUB subtiles of 32 rows). The workgroup streams the
-// whole key range in blocks of BN keys; each K block and V^T block is staged
-// once in LDS (a ring of slots) and read by every wave, and every wave keeps
-// its Q fragments, O accumulators and softmax statistics in registers for the
-// whole key loop. The ping-pong body also masks ragged query and key tails,
-// writes the per-row log-sum-exp on request, applies an optional causal mask
-// (a query tile then streams only the key blocks up to its diagonal), and has
-// a capture variant that records the per-block softmax statistics.
+// op_kernel/panel_kernel.h:264-274): a query tile is BM = 256 query rows of
+// one (batch, head), 8 waves x 32 rows. The attention kernel is persistent:
+// one workgroup per CU takes tiles from a counter until none are left. For a
+// tile it streams the whole key range in blocks of BN keys; each K block and
+// V^T block is staged once in LDS (a ring of slots) and read by every wave,
+// and every wave keeps its Q fragments, O accumulators and softmax
+// statistics in registers for the whole key loop. Ragged query and key tails
+// are masked, the per-row log-sum-exp is written on request, and an optional
+// causal mask makes a tile stream only the key blocks up to its diagonal.
+// Separate instantiations add the capture (per-block softmax statistics),
+// trace (per-tile clock stamps) and synchronous debug modes.
 //
 // Matrix products run transposed so the softmax is lane-local:
 //   S^T = K Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS, B = Q^T
@@ -30,10 +31,9 @@
 // Online softmax in base 2 with the scale folded in (c = scale*log2(e)):
 //   m' = max(m, rowmax(S)),  alpha = 2^((m - m') c),  P = 2^(S c - m' c),
 //   l' = alpha l + rowsum(P16),  O' = alpha O + P16 V
-// where P16 is P rounded to FP16 (the MFMA operand). With the FP32 O the row
-// sum is taken over the same rounded values, so numerator and denominator
-// use identical weights; with the FP16 O it is taken over the unrounded FP32
-// P (cheaper there; the difference is within 2^-11 relative per term).
+// where P16 is P rounded to FP16 (the MFMA operand). The row sum is taken
+// over the same rounded values, so numerator and denominator use identical
+// weights.
 // Semantics follow the reference's FP32 vector softmax
 // (project/op_kernel/online_softmax.h:86-224, vector_output.h:22-86 of the
 // FP32 variant) and, for FA_ACC_FP16, its FP16-O merge (vector_output.h:

@@ -381,6 +381,41 @@ def test_full_size_sampled_rows(ops, idx, acc):
     torch.cuda.empty_cache()
 
 
+LONG = [
+    # (B, Hq, Hkv, Nq, Nk, causal): a million keys (ragged, 32-bit key
+    # offsets near their largest in any test), and a million query rows.
+    (1, 4, 1, 512, 1_048_573, "none"),
+    (1, 4, 1, 512, 1_048_573, "bottom_right"),
+    (1, 2, 1, 1_048_573, 640, "none"),
+]
+
+
+@pytest.mark.parametrize("acc", ["fp32", "fp16"])
+@pytest.mark.parametrize("shape", LONG, ids=lambda s: "x".join(map(str, s)))
+def test_long_sequences_sampled_rows(library_path, shape, acc):
+    b, hq, hkv, nq, nk, causal = shape
+    say(f"case long {shape} acc={acc}: generating inputs")
+    g = torch.Generator().manual_seed(nq ^ nk)
+    q = torch.randn(b, hq, nq, 128, generator=g).half()
+    k = torch.randn(b, hkv, nk, 128, generator=g).half()
+    v = torch.randn(b, hkv, nk, 128, generator=g).half()
+    op = Operator(library_path, AttentionConfig(acc=acc, causal=causal))
+    say(f"case long {shape} acc={acc}: launching")
+    out, lse = op(q.cuda(), k.cuda(), v.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    rows = orc.sample_rows(q.shape, 24, seed=nq + nk)       # both ends of the range included
+    idx = torch.tensor(rows)
+    got = out[idx[:, 0], idx[:, 1], idx[:, 2]].float().cpu().numpy()
+    exact = orc.attention_rows_f64(q, k, v, rows, causal=causal)
+    wabs = orc.attention_rows_f64(q, k, v.abs(), rows, causal=causal)
+    worst = check(got, exact, acc, f"long {shape}", wabs)
+    assert worst <= ATOL[acc]
+    got_lse = lse[idx[:, 0], idx[:, 1], idx[:, 2]].cpu().numpy()
+    check_lse(got_lse, orc.lse_rows_f64(q, k, rows, causal=causal), f"long {shape}")
+    del out, lse
+    torch.cuda.empty_cache()
+
+
 def test_golden_fixture(ops):
     say("case golden fixture B1_S256_Q2_KV1")
     from pathlib import Path

@@ -20,6 +20,9 @@
 //   MODE 3  each A operand read from LDS feeds two MFMAs (with different B
 //           operands): the LDS traffic a wave with 64 query rows would
 //           have, half of the attention kernel's.
+//   MODE 4  both operands of every MFMA read from LDS (2 KiB per MFMA and
+//           wave, twice the attention kernel's traffic): how close LDS
+//           bandwidth comes to limiting the matrix pipe.
 //
 // Operands are FP16 values supplied by the caller (random normal data, so the
 // datapath toggles as it does on real inputs). Every wave keeps four
@@ -77,6 +80,23 @@ fa_mfma_ceiling_kernel(const _Float16* __restrict__ operands, float* __restrict_
     if constexpr (MODE == 0) {
 #pragma unroll
       for (int n = 0; n < kMfmaPerIter; ++n) acc[n & 3] = mfma32(a[n >> 2], b[n & 3], acc[n & 3]);
+    } else if constexpr (MODE == 4) {
+      h8 fa[4], fb[4];
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        fa[f] = *reinterpret_cast<const h8*>(base + f * 1024);
+        fb[f] = *reinterpret_cast<const h8*>(base + (8 + f) * 1024);
+      }
+#pragma unroll
+      for (int n = 0; n < kMfmaPerIter; ++n) {
+        const h8 x = fa[n & 3], y = fb[n & 3];
+        if (n + 4 < kMfmaPerIter) {
+          fa[n & 3] = *reinterpret_cast<const h8*>(base + ((n + 4) & 7) * 1024);
+          fb[n & 3] = *reinterpret_cast<const h8*>(base + (8 + ((n + 4) & 7)) * 1024);
+        }
+        acc[n & 3] = mfma32(x, y, acc[n & 3]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     } else if constexpr (MODE == 3) {
       h8 fr[4];
 #pragma unroll
@@ -144,13 +164,13 @@ uint64_t fa_ceiling_flops_per_workgroup(int iters) {
 }
 
 // Launch the ceiling kernel: mode 0 (register operands), 1 (LDS-fed A
-// operand), 2 (LDS-fed A operand and the softmax's VALU mix) or 3 (one LDS
-// read per two MFMAs); operands = 8192 FP16 values (16-byte aligned), out = workgroups
+// operand), 2 (LDS-fed A operand and the softmax's VALU mix), 3 (one LDS
+// read per two MFMAs) or 4 (both operands from LDS); operands = 8192 FP16 values (16-byte aligned), out = workgroups
 // x 512 floats, trace = workgroups x 8 words or NULL. Returns 0, or 1 for
 // bad arguments, 2 when the launch is rejected.
 int fa_ceiling_mfma(int mode, int workgroups, int iters, const void* operands, float* out,
                     uint64_t* trace, void* stream) {
-  if (mode < 0 || mode > 3 || workgroups <= 0 || iters <= 0 || !operands || !out) return 1;
+  if (mode < 0 || mode > 4 || workgroups <= 0 || iters <= 0 || !operands || !out) return 1;
   if ((reinterpret_cast<uintptr_t>(operands) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(trace)) & 15)
     return 1;
@@ -159,7 +179,8 @@ int fa_ceiling_mfma(int mode, int workgroups, int iters, const void* operands, f
   const void* fns[] = {reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<0>),
                        reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<1>),
                        reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<2>),
-                       reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<3>)};
+                       reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<3>),
+                       reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<4>)};
   const void* fn = fns[mode];
   return hipLaunchKernel(fn, dim3((unsigned)workgroups), dim3(kThreads), args, 0,
                          static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : 2;

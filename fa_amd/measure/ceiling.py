@@ -11,8 +11,9 @@ current stream after warmup launches:
   softmax's VALU instruction mix beside every MFMA (mode 2: one exponential
   and three other FP32 operations, independent of the MFMAs -- the forward's
   work without its dependencies and barriers), or with each LDS read
-  feeding two MFMAs (mode 3: half the LDS traffic). Its trace records give
-  the clock it ran at.
+  feeding two MFMAs (mode 3: half the LDS traffic), or with both operands
+  read from LDS (mode 4: twice the traffic, a test of LDS bandwidth). Its
+  trace records give the clock it ran at.
 * ``gemm`` -- torch's FP16 matrix product (hipBLASLt) on large square and
   rectangular shapes, the rate a tuned vendor GEMM reaches.
 
@@ -35,7 +36,7 @@ import sys
 GEMM_SHAPES = ((8192, 8192, 8192), (8192, 8192, 16384), (16384, 16384, 8192))
 # MFMA loop modes of libfa_ceiling.so and their labels in measure()'s result.
 MODES = ((0, "registers"), (1, "lds_operand"), (2, "lds_operand_softmax_valu"),
-         (3, "lds_operand_read_per_two"))
+         (3, "lds_operand_read_per_two"), (4, "both_operands_lds"))
 
 
 def _library():
@@ -145,7 +146,8 @@ def main(argv=None) -> int:
         print(lines[-1], flush=True)
     for mode, label in ((0, "operands in registers"), (1, "A operand read from LDS"),
                         (2, "A operand from LDS + the softmax's VALU mix"),
-                        (3, "one LDS operand read per two MFMAs")):
+                        (3, "one LDS operand read per two MFMAs"),
+                        (4, "both operands read from LDS")):
         rate, records = mfma_loop(mode)
         if args.records:
             import numpy as np

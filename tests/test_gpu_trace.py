@@ -66,7 +66,7 @@ def test_ceiling_kernel_runs_and_reports_a_clock():
     lib = ceiling._library()
     # Host-side rejections (nothing is launched): unknown mode, no
     # workgroups, misaligned operands.
-    assert lib.fa_ceiling_mfma(4, 1, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
+    assert lib.fa_ceiling_mfma(5, 1, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
     assert lib.fa_ceiling_mfma(-1, 1, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
     assert lib.fa_ceiling_mfma(0, 0, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
     assert lib.fa_ceiling_mfma(0, 1, 1, C.c_void_p(24), C.c_void_p(16), None, None) == 1

@@ -81,6 +81,13 @@ SIGNATURES = {
                               C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
     "fa_fwd_noalloc": (C.c_int, [C.POINTER(FaProblem), C.c_void_p, C.c_void_p, C.c_void_p,
                                  C.c_void_p, C.c_void_p]),
+    "fa_fwd_split_count": (C.c_int, [C.POINTER(FaProblem), C.c_int32, C.c_int32,
+                                     C.POINTER(C.c_int32)]),
+    "fa_fwd_split_workspace_bytes": (C.c_int, [C.POINTER(FaProblem), C.c_int32,
+                                               C.POINTER(C.c_uint64)]),
+    "fa_fwd_split": (C.c_int, [C.POINTER(FaProblem), C.c_int32, C.POINTER(FaStrides), C.c_void_p,
+                               C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                               C.c_uint64, C.c_void_p]),
     "fa_fwd_tile": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "fa_fwd_select": (C.c_int, [C.POINTER(FaProblem), C.POINTER(C.c_int32)]),
     "fa_kernel_count": (C.c_int, []),
@@ -110,13 +117,18 @@ class AttentionConfig:
     it ran and its clock stamps (the reference kernel's ``trace`` output),
     and the synchronous debug mode (``fa_fwd_sync``: poisoned staging
     buffers, no load/compute overlap; the reference's ``SYNCHRONOUS`` build
-    flag), whose output must equal the production kernel's bit for bit."""
+    flag), whose output must equal the production kernel's bit for bit.
+    ``splits`` selects the key-split forward (``fa_fwd_split``): None (the
+    default) runs one work item per query tile, 0 lets the library choose a
+    split count, n >= 1 asks for n parts of every tile's key range (1 is the
+    unsplit forward)."""
     acc: str = "fp32"
     kernel: int = 0
     capture: bool = False
     causal: str = "none"
     trace: bool = False
     sync: bool = False
+    splits: "int | None" = None
 
     def __post_init__(self):
         if self.acc not in FA_ACC:
@@ -133,6 +145,12 @@ class AttentionConfig:
             raise ValueError("sync must be a bool")
         if self.trace + self.capture + self.sync > 1:
             raise ValueError("capture, trace and sync are separate kernels; pick one")
+        if self.splits is not None:
+            if not isinstance(self.splits, int) or isinstance(self.splits, bool) \
+                    or not 0 <= self.splits <= 1024:
+                raise ValueError("splits must be None or an int in 0..1024")
+            if self.capture or self.trace or self.sync:
+                raise ValueError("the key-split forward has no capture, trace or sync mode")
 
 
 def make_problem(q_shape, k_shape, scale, config):
@@ -176,6 +194,17 @@ class Operator:
 
     def kernel_name(self, q_shape, k_shape):
         return self.lib.fa_kernel_name(self.kernel(q_shape, k_shape)).decode()
+
+    def split_count(self, q_shape, k_shape, cus=0):
+        """Key-range parts per query tile the key-split forward would run
+        (``config.splits`` resolved; ``cus`` = 0: the current device)."""
+        if self.config.splits is None:
+            return 1
+        prob = make_problem(q_shape, k_shape, 1.0, self.config)
+        n = C.c_int32()
+        self.check(self.lib.fa_fwd_split_count(C.byref(prob), self.config.splits, cus,
+                                               C.byref(n)), "split")
+        return n.value
 
     def validate(self, q, k, v):
         import torch
@@ -258,7 +287,13 @@ class Operator:
             raise ValueError("scale must be finite and positive")
         prob = make_problem(q.shape, k.shape, scale, self.config)
         size = C.c_uint64()
-        self.check(self.lib.fa_fwd_workspace_bytes(C.byref(prob), C.byref(size)), "prepare")
+        splits = self.config.splits
+        if splits is None:
+            self.check(self.lib.fa_fwd_workspace_bytes(C.byref(prob), C.byref(size)), "prepare")
+        else:
+            with torch.cuda.device(q.device):
+                self.check(self.lib.fa_fwd_split_workspace_bytes(C.byref(prob), splits,
+                                                                 C.byref(size)), "prepare")
         out = self.buffers_for(q, k)
         capture = self.config.capture
         lse = self.buffers_for(q, k, lse=True) if (return_lse or capture) else None
@@ -276,10 +311,16 @@ class Operator:
             common = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr())
             tail = (self.workspace.data_ptr(), self.workspace.numel(),
                     C.c_void_p(stream.cuda_stream))
+            st = None
             if strided:
                 st = FaStrides()
                 for name, t in (("q", q), ("k", k), ("v", v), ("o", out)):
                     getattr(st, name)[:] = t.stride()[:3]
+            if splits is not None:
+                status = self.lib.fa_fwd_split(C.byref(prob), splits,
+                                               C.byref(st) if st is not None else None, *common,
+                                               lse.data_ptr() if lse is not None else None, *tail)
+            elif strided:
                 status = self.lib.fa_fwd_strided(C.byref(prob), C.byref(st), *common,
                                                  lse.data_ptr() if lse is not None else None,
                                                  *tail)

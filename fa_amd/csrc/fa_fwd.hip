@@ -73,9 +73,12 @@ constexpr float LN2 = 0.6931471805599453f;
 // debug mode: every tile's LDS ring starts poisoned with FP16 NaN and each
 // phase's loads complete before the phase ends, so a read of LDS no load has
 // filled, or a race between the loads and the operand reads, changes the
-// output. All three are separate kernels.
-enum KernelMode { MODE_RUN = 0, MODE_CAPTURE = 1, MODE_TRACE = 2, MODE_SYNC = 3 };
-constexpr int kModes = 4;
+// output. Split is the key-split mode: a work item is one query tile and one
+// of `splits` contiguous parts of its key range, and it writes that part's
+// normalised FP32 O and log-sum-exp for a merge kernel to combine. All four
+// are separate kernels.
+enum KernelMode { MODE_RUN = 0, MODE_CAPTURE = 1, MODE_TRACE = 2, MODE_SYNC = 3, MODE_SPLIT = 4 };
+constexpr int kModes = 5;
 // FP16 quiet NaN in both halves of a 32-bit word: the poison of sync mode.
 constexpr uint32_t NAN16X2 = 0x7e007e00u;
 
@@ -107,7 +110,11 @@ constexpr int TRACE_WORDS = 8;
 // (causal_off = 0 aligns the mask top-left, Nk - Nq bottom-right); a row that
 // sees no key gets O = 0 and lse = -inf. qs, ks and os are the element
 // strides of q, of the K buffer read (the caller's k, or its padded
-// contiguous copy) and of o.
+// contiguous copy) and of o. In split mode (splits >= 2) the kernel writes,
+// instead of o and lse, each part's O normalised by its own row sum into
+// opart (FP32 [splits][B * Hq * Nq][128]) and the part's natural-log
+// log-sum-exp into lpart (FP32 [splits][B * Hq * Nq]; -inf for a part in
+// which the row sees no key, whose opart row is left unwritten).
 struct Strides {
   int64_t b, h, n;   // batch, head and row strides in elements; the 128 dims are contiguous
 };
@@ -125,6 +132,10 @@ struct FaArgs {
   int causal, causal_off;
   float c;
   Strides qs, ks, os;
+  // Split mode only (last, so the other modes' argument offsets do not move).
+  float* opart;
+  float* lpart;
+  int splits;          // key-range parts per tile
 };
 
 // Row n of head h of batch b of a strided [B, H, N, 128] tensor.
@@ -224,6 +235,52 @@ __global__ void __launch_bounds__(256) fa_poison_kernel(u32x4* p, uint64_t n16) 
     p[i] = nan;
 }
 
+// Split mode's second kernel: for every query row, combines the parts'
+// results O_s (normalised by the part's own row sum) and lse_s into
+//   O = sum_s w_s O_s / sum_s w_s,  lse = M + ln sum_s w_s,
+//   w_s = exp(lse_s - M),  M = max_s lse_s,
+// the log-sum-exp algebra of the online softmax applied once across parts.
+// A part whose lse is -inf (the row sees none of its keys) has no weight and
+// its O row is not read; a row that sees no key at all gets O = 0 and
+// lse = -inf. 32 lanes per row (4 of the 128 dims each), 8 rows per
+// 256-thread block, grid-stride over the rows = B * Hq * Nq; o is written
+// through its strides, lse (may be null) contiguously.
+__global__ void __launch_bounds__(256) fa_merge_kernel(const float* __restrict__ opart,
+                                                       const float* __restrict__ lpart,
+                                                       _Float16* __restrict__ o,
+                                                       float* __restrict__ lse, int splits,
+                                                       int64_t rows, int heads_q, int seq_q,
+                                                       Strides os) {
+  const int sub = threadIdx.x & 31;
+  const int64_t step = (int64_t)gridDim.x * 8;
+  for (int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5); row < rows; row += step) {
+    float mx = -INFINITY;
+    for (int s = 0; s < splits; ++s) mx = fmaxf(mx, lpart[s * rows + row]);
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, wsum = 0.f;
+    if (mx != -INFINITY) {
+      for (int s = 0; s < splits; ++s) {
+        const float ls = lpart[s * rows + row];
+        if (ls == -INFINITY) continue;
+        const float w = __builtin_amdgcn_exp2f((ls - mx) * (float)LOG2E);
+        const float4 v = *reinterpret_cast<const float4*>(opart + ((size_t)s * rows + row) * HD + 4 * sub);
+        a0 = __builtin_fmaf(w, v.x, a0);
+        a1 = __builtin_fmaf(w, v.y, a1);
+        a2 = __builtin_fmaf(w, v.z, a2);
+        a3 = __builtin_fmaf(w, v.w, a3);
+        wsum += w;
+      }
+    }
+    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+    const int64_t bh = row / seq_q;
+    const int i = (int)(row - bh * seq_q);
+    const int b = (int)(bh / heads_q), h = (int)(bh - (int64_t)b * heads_q);
+    const h4 out = {(_Float16)(a0 * inv), (_Float16)(a1 * inv), (_Float16)(a2 * inv),
+                    (_Float16)(a3 * inv)};
+    *reinterpret_cast<h4*>(row_at(o, os, b, h, i) + 4 * sub) = out;
+    if (lse && sub == 0) lse[row] = wsum > 0.f ? mx + __builtin_amdgcn_logf(wsum) * LN2 : -INFINITY;
+  }
+}
+
 // Trace mode: thread 0 writes the tile's record (layout at TRACE_WORDS)
 // with the start stamps real0/clk0 and stamps taken now.
 __device__ __forceinline__ void trace_record(const FaArgs& args, int tile, uint64_t real0,
@@ -270,10 +327,11 @@ __device__ __forceinline__ void trace_record(const FaArgs& args, int tile, uint6
 // rescale runs only on the rare blocks where some row of the wave needs it.
 // With TAU = 0 the max tracks every increase (FP16 O must not grow).
 template <bool ACC16, int BN, int NS, int MODE>
-__device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
+__device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, const int split) {
   constexpr bool CAPTURE = MODE == MODE_CAPTURE;
   constexpr bool TRACE = MODE == MODE_TRACE;
   constexpr bool SYNC = MODE == MODE_SYNC;
+  constexpr bool SPLIT = MODE == MODE_SPLIT;
   uint64_t real0 = 0, clk0 = 0;
   if constexpr (TRACE) {
     real0 = __builtin_amdgcn_s_memrealtime();
@@ -368,6 +426,19 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
     const int kend = min(qt * BM + BM, seq_q) + args.causal_off;   // keys [0, kend) are seen
     nblk = kend <= 0 ? 0 : min(nblk, (kend + BN - 1) / BN);
   }
+  // Split mode: this work item streams key blocks [kb0, kb1) of the tile
+  // (part `split` of args.splits near-equal parts of the key blocks), with
+  // the loads, limits and masks below relative to key kb0 * BN.
+  int kb0 = 0;
+  if constexpr (SPLIT) {
+    const int nbt = seq_k / BN;
+    kb0 = (int)((int64_t)split * nbt / args.splits);
+    const int kb1 = (int)((int64_t)(split + 1) * nbt / args.splits);
+    nblk = max(0, min(nblk, kb1) - kb0);
+    klim -= kb0 * BN;
+    klim_w -= kb0 * BN;
+  }
+  const size_t part = (size_t)split * ((size_t)nbh * seq_q) + grow;   // split mode: partial row
   if (nblk == 0) {
     // No row of this tile sees a key (bottom-right mask, Nq > Nk): O = 0 and
     // lse = -inf. Uniform over the workgroup, before any barrier or load.
@@ -384,6 +455,10 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
     }
     if constexpr (TRACE) trace_record(args, tile, real0, clk0, 0, BN);
     if (!row_ok) return;
+    if constexpr (SPLIT) {
+      if (hf == 0) args.lpart[part] = -INFINITY;
+      return;
+    }
     if (args.lse && hf == 0) args.lse[grow] = -INFINITY;
     const h4 zero = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
 #pragma unroll
@@ -424,10 +499,11 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
   // read (lgkmcnt(0)) after each one, which drained the operand prefetch
   // of the MFMA step; buffer loads are counted on vmcnt only.
   constexpr int RSRC_WORD3 = 0x00020000;   // gfx9 raw-buffer descriptor: 32-bit data format
-  const __amdgpu_buffer_rsrc_t krsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)kp, (short)0, (seq_k - 1) * krow + HD * 2, RSRC_WORD3);
-  const __amdgpu_buffer_rsrc_t vrsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)vp, (short)0, seq_k * (HD * 2), RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(kp + (size_t)kb0 * BN * args.ks.n), (short)0, (seq_k - kb0 * BN - 1) * krow + HD * 2,
+      RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(vp + kb0 * BN), (short)0, seq_k * (HD * 2) - kb0 * (BN * 2), RSRC_WORD3);
   // DMA instruction m of this wave for K block kb -> ring slot ks and V^T
   // block vb -> slot vs. Branch free: the K/V^T choice is a select on
   // wave-uniform values; only a wave's last instruction can be absent.
@@ -796,6 +872,21 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile) {
   const float l = half_sum(lsum);
   const float inv = l > 0.f ? 1.f / l : 0.f;
   if (!row_ok) return;
+  if constexpr (SPLIT) {
+    // This part's O / l in FP32 and its log-sum-exp (-inf, with O = 0, for a
+    // row that sees no key of the part).
+    if (hf == 0) args.lpart[part] = (__builtin_amdgcn_logf(l) + m * c) * LN2;
+    float* prow = args.opart + part * HD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 val = {acc[dt][4 * g] * inv, acc[dt][4 * g + 1] * inv, acc[dt][4 * g + 2] * inv,
+                            acc[dt][4 * g + 3] * inv};
+        *reinterpret_cast<float4*>(prow + dt * 32 + 8 * g + 4 * hf) = val;
+      }
+    return;
+  }
   if (args.lse && hf == 0) args.lse[grow] = (__builtin_amdgcn_logf(l) + m * c) * LN2;
   _Float16* orow = row_at(o, args.os, b, h, rowc);
 #pragma unroll
@@ -850,17 +941,29 @@ __device__ __forceinline__ FaArgs load_args(uint64_t addr) {
   r.qs = load_strides(a->qs);
   r.ks = load_strides(a->ks);
   r.os = load_strides(a->os);
+  r.opart = a->opart;
+  r.lpart = a->lpart;
+  r.splits = a->splits;
   return r;
 }
 
 template <bool ACC16, int BN, int NS, int MODE>
 __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   __shared__ int claimed;
+  // Work items: query tiles, or in split mode (tile, part) pairs, the parts
+  // of one tile consecutive.
+  int items = args.tiles;
+  if constexpr (MODE == MODE_SPLIT) items *= args.splits;
   for (;;) {
     if (threadIdx.x == 0) claimed = atomicAdd(args.next_tile, 1);
     __syncthreads();
-    const int tile = __builtin_amdgcn_readfirstlane(claimed);
-    if (tile >= args.tiles) break;
+    const int item = __builtin_amdgcn_readfirstlane(claimed);
+    if (item >= items) break;
+    int tile = item, split = 0;
+    if constexpr (MODE == MODE_SPLIT) {
+      tile = item / args.splits;
+      split = item - tile * args.splits;
+    }
     // Each tile reloads the arguments from the kernel-argument segment
     // through an address the compiler cannot follow across iterations: kept
     // from one tile to the next, all of them would stay live in scalar
@@ -868,7 +971,7 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
     // pressure spills.
     uint64_t addr = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
     asm volatile("" : "+s"(addr));
-    fa_pp_tile<ACC16, BN, NS, MODE>(load_args(addr), tile);
+    fa_pp_tile<ACC16, BN, NS, MODE>(load_args(addr), tile, split);
     // Every wave has read `claimed` (and finished with the LDS ring) before
     // thread 0 claims the next tile.
     __syncthreads();
@@ -882,7 +985,7 @@ constexpr int pp_lds_bytes(int bn, int ns) { return ns * (bn * (HD * 2 + 16) + H
 // Device entry points, one per accumulation variant. Their names contain the
 // backend names of the two accumulation variants, which is how a profile
 // attributes kernel time to a backend. Template parameters: BN keys per
-// block, NS slots in the LDS ring, MODE (production, capture, trace or sync;
+// block, NS slots in the LDS ring, MODE (production, capture, trace, sync or split;
 // each mode is a separate kernel, so the production kernels carry none of
 // the debug code). 8 waves of 64 lanes, two per SIMD.
 template <int BN, int NS, int MODE>
@@ -916,9 +1019,11 @@ constexpr uint64_t kCounterBytes = 256;
   TileConfig {                                                                              \
     NAME, BN, pp_lds_bytes(BN, NS), {                                                       \
       {&hip_fa_fp32acc_kernel<BN, NS, MODE_RUN>, &hip_fa_fp32acc_kernel<BN, NS, MODE_CAPTURE>, \
-       &hip_fa_fp32acc_kernel<BN, NS, MODE_TRACE>, &hip_fa_fp32acc_kernel<BN, NS, MODE_SYNC>}, \
+       &hip_fa_fp32acc_kernel<BN, NS, MODE_TRACE>, &hip_fa_fp32acc_kernel<BN, NS, MODE_SYNC>,  \
+       &hip_fa_fp32acc_kernel<BN, NS, MODE_SPLIT>},                                            \
       {&hip_fa_fp16acc_kernel<BN, NS, MODE_RUN>, &hip_fa_fp16acc_kernel<BN, NS, MODE_CAPTURE>, \
-       &hip_fa_fp16acc_kernel<BN, NS, MODE_TRACE>, &hip_fa_fp16acc_kernel<BN, NS, MODE_SYNC>}  \
+       &hip_fa_fp16acc_kernel<BN, NS, MODE_TRACE>, &hip_fa_fp16acc_kernel<BN, NS, MODE_SYNC>,  \
+       &hip_fa_fp16acc_kernel<BN, NS, MODE_SPLIT>}                                             \
     }                                                                                       \
   }
 
@@ -1004,6 +1109,108 @@ uint64_t grid_size(const fa_problem* p) {
   return (uint64_t)(p->batch * p->heads_q) * (uint64_t)((p->seq_q + kRows - 1) / kRows);
 }
 
+// Split mode's partial results, after the tile counter in the workspace:
+// the parts' log-sum-exp (FP32 [splits][R], R = B * Hq * Nq) from a 256-byte
+// boundary, then their O (FP32 [splits][R][128]).
+struct SplitLayout {
+  uint64_t lpart_offset, opart_offset, end;
+};
+SplitLayout split_layout(const fa_problem* p, const KeyLayout& lay, int splits) {
+  const uint64_t rows = (uint64_t)(p->batch * p->heads_q) * (uint64_t)p->seq_q;
+  SplitLayout sl;
+  sl.lpart_offset = lay.workspace_bytes();   // a multiple of 256
+  sl.opart_offset = sl.lpart_offset + (splits * rows * sizeof(float) + 255) / 256 * 256;
+  sl.end = sl.opart_offset + splits * rows * HD * sizeof(float);
+  return sl;
+}
+
+// Largest accepted split count (fa_fwd_split's splits argument).
+constexpr int kMaxSplits = 1024;
+// Split counts the automatic choice considers: every count up to
+// kAutoSplitMax without a mask (the model is a closed form there), these
+// with a causal mask (the model sums over the tiles).
+constexpr int kAutoSplitMax = 64;
+constexpr int kAutoSplitsCausal[] = {2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64};
+
+// Modelled duration of a launch whose tiles' key ranges are cut into s
+// parts, in units of one key block's time on one workgroup. A work item
+// costs its key blocks plus kItemOverhead (pipeline fill and drain,
+// epilogue), an empty item (a causal part past the diagonal) almost nothing.
+// Equal items (full attention) run in ceil(items / cus) rounds; unequal ones
+// (causal) are bounded by max(total / cus, longest item), which the work
+// queue, handing out the longest tiles first, comes close to. A split launch
+// adds the merge kernel: it reads every part's O and lse and writes O, at
+// kMergeBytesPerSecond.
+constexpr double kItemOverhead = 1.5;
+constexpr double kEmptyItem = 0.1;
+constexpr double kMergeBytesPerSecond = 4.0e12;
+double split_cost(const fa_problem* p, const TileConfig* tile, const KeyLayout& lay, int s, int cus) {
+  const int bn = tile->keys;
+  const int64_t nbt = lay.nk_pad / bn;
+  const int64_t nbh = p->batch * p->heads_q, tiles_q = (p->seq_q + kRows - 1) / kRows;
+  const double items = (double)(nbh * tiles_q) * s;
+  double t = 0.0;
+  if (p->causal == FA_CAUSAL_NONE) {
+    const double per = (double)((nbt + s - 1) / s) + kItemOverhead;
+    t = ceil(items / cus) * per;
+  } else {
+    const int64_t off = p->causal == FA_CAUSAL_BOTTOM_RIGHT ? p->seq_k - p->seq_q : 0;
+    double total = 0.0, longest = 0.0;
+    for (int64_t r = 0; r < tiles_q; ++r) {
+      const int64_t kend = std::min<int64_t>((r + 1) * kRows, p->seq_q) + off;
+      const int64_t vis = kend <= 0 ? 0 : std::min<int64_t>(nbt, (kend + bn - 1) / bn);
+      for (int i = 0; i < s; ++i) {
+        const int64_t b0 = i * nbt / s, b1 = (i + 1) * nbt / s;
+        const int64_t nb = std::max<int64_t>(0, std::min(vis, b1) - b0);
+        const double cost = nb > 0 ? nb + kItemOverhead : kEmptyItem;
+        total += cost * nbh;
+        longest = std::max(longest, cost);
+      }
+    }
+    t = std::max(total / cus, longest);
+  }
+  if (s > 1) {
+    const double rows = (double)nbh * p->seq_q;
+    const double bytes = rows * (s * (HD * 4.0 + 4.0) + HD * 2.0 + 4.0);
+    const double block_seconds = bn == 128 ? 3.4e-6 : 1.8e-6;
+    t += bytes / kMergeBytesPerSecond / block_seconds;
+  }
+  return t;
+}
+
+// Effective split count for a requested one: 0 picks the count with the
+// shortest modelled launch (splitting only when that beats one pass over the
+// keys by 10 %: tiles must leave CUs idle), n >= 1 is clamped to the tile's
+// key blocks (every part then has at least one).
+int resolve_splits(const fa_problem* p, const TileConfig* tile, const KeyLayout& lay,
+                   int requested, int cus, int* out) {
+  if (requested < 0 || requested > kMaxSplits || cus <= 0) return FA_ERR_SPLIT;
+  const int64_t nbt = lay.nk_pad / tile->keys;
+  int s = (int)std::min<int64_t>(requested, nbt);
+  if (requested == 0) {
+    s = 1;
+    if (grid_size(p) < 2 * (uint64_t)cus) {
+      double best = 0.9 * split_cost(p, tile, lay, 1, cus);
+      auto consider = [&](int c) {
+        if (c > nbt) return;
+        const double t = split_cost(p, tile, lay, c, cus);
+        if (t < best) {
+          best = t;
+          s = c;
+        }
+      };
+      if (p->causal == FA_CAUSAL_NONE) {
+        for (int c = 2; c <= kAutoSplitMax; ++c) consider(c);
+      } else {
+        for (int c : kAutoSplitsCausal) consider(c);
+      }
+    }
+  }
+  if ((int64_t)grid_size(p) * s >= ((int64_t)1 << 30)) return FA_ERR_GEOMETRY;
+  *out = std::max(s, 1);
+  return FA_OK;
+}
+
 // Strides of a contiguous [B, H, N, 128] tensor.
 Strides contiguous(int64_t heads, int64_t seq) { return Strides{heads * seq * HD, seq * HD, HD}; }
 
@@ -1071,6 +1278,8 @@ struct Extras {
   uint64_t* trace = nullptr;
   uint64_t trace_count = 0;
   bool sync = false;
+  bool split = false;        // fa_fwd_split: split the key range of every tile
+  int splits = 0;            // requested parts (0 = automatic)
 };
 
 int launch(const fa_problem* p, const fa_strides* strides, const void* q, const void* k,
@@ -1091,19 +1300,38 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
     vs = strides_of(strides->v);
     os = strides_of(strides->o);
   }
-  if (!workspace || workspace_bytes < lay.workspace_bytes()) return FA_ERR_WORKSPACE;
+  // The automatic split count depends on the device's CU count; an explicit
+  // one does not, so its errors come before any device query.
+  int cus = 0;
+  int splits = 1;
+  if (ex.split) {
+    if (ex.splits == 0) {
+      rc = device_cus(&cus);
+      if (rc) return rc;
+    }
+    rc = resolve_splits(p, tile, lay, ex.splits, cus ? cus : 1, &splits);
+    if (rc) return rc;
+  }
+  const SplitLayout sl = split_layout(p, lay, splits);
+  if (!workspace || workspace_bytes < (splits > 1 ? sl.end : lay.workspace_bytes()))
+    return FA_ERR_WORKSPACE;
   for (const void* ptr : {q, k, v, (const void*)o, (const void*)workspace, (const void*)ex.lse,
                           (const void*)ex.stats, (const void*)ex.trace})
     if (reinterpret_cast<uintptr_t>(ptr) & 15) return FA_ERR_ALIGN;
   if (ex.stats && ex.stats_count < capture_count(p, tile, lay)) return FA_ERR_CAPTURE;
   if (ex.trace && ex.trace_count < grid_size(p) * TRACE_WORDS) return FA_ERR_TRACE;
   const int acc = p->acc == FA_ACC_FP16 ? 1 : 0;
-  const int mode = ex.stats ? MODE_CAPTURE : ex.trace ? MODE_TRACE : ex.sync ? MODE_SYNC : MODE_RUN;
+  const int mode = splits > 1 ? MODE_SPLIT
+                   : ex.stats ? MODE_CAPTURE
+                   : ex.trace ? MODE_TRACE
+                   : ex.sync  ? MODE_SYNC
+                              : MODE_RUN;
   rc = ensure_lds_limit(tile, acc, mode);
   if (rc) return rc;
-  int cus = 0;
-  rc = device_cus(&cus);
-  if (rc) return rc;
+  if (!cus) {
+    rc = device_cus(&cus);
+    if (rc) return rc;
+  }
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   _Float16* vt = static_cast<_Float16*>(workspace);
@@ -1142,8 +1370,11 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
   args.lse = ex.lse;
   args.stats = ex.stats;
   args.trace = ex.trace;
+  args.opart = reinterpret_cast<float*>(static_cast<char*>(workspace) + sl.opart_offset);
+  args.lpart = reinterpret_cast<float*>(static_cast<char*>(workspace) + sl.lpart_offset);
   args.next_tile = next_tile;
   args.tiles = (int)grid_size(p);
+  args.splits = splits;
   args.heads_q = (int)p->heads_q;
   args.group = (int)(p->heads_q / p->heads_kv);
   args.seq_q = (int)p->seq_q;
@@ -1157,11 +1388,25 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
   args.ks = lay.pad_k ? contiguous(p->heads_kv, lay.nk_pad) : ks;
   void* attn_args[] = {&args};
   // One workgroup per CU (the LDS ring leaves room for no second one), never
-  // more workgroups than tiles.
-  const unsigned grid = (unsigned)std::min<uint64_t>(grid_size(p), (uint64_t)cus);
+  // more workgroups than work items.
+  const unsigned grid = (unsigned)std::min<uint64_t>(grid_size(p) * splits, (uint64_t)cus);
   if (hipLaunchKernel(reinterpret_cast<const void*>(tile->fn[acc][mode]), dim3(grid),
                       dim3(kThreads), attn_args, tile->lds, st) != hipSuccess)
     return FA_ERR_LAUNCH;
+  if (splits > 1) {
+    const float* opart = args.opart;
+    const float* lpart = args.lpart;
+    _Float16* out = args.o;
+    float* lse = ex.lse;
+    int nsplit = splits;
+    int64_t rows = p->batch * p->heads_q * p->seq_q;
+    int heads_q = (int)p->heads_q, seq_q = (int)p->seq_q;
+    void* merge_args[] = {&opart, &lpart, &out, &lse, &nsplit, &rows, &heads_q, &seq_q, &os};
+    const unsigned blocks = (unsigned)std::min<int64_t>((rows + 7) / 8, (int64_t)1 << 20);
+    if (hipLaunchKernel(reinterpret_cast<const void*>(&fa_merge_kernel), dim3(blocks), dim3(256),
+                        merge_args, 0, st) != hipSuccess)
+      return FA_ERR_LAUNCH;
+  }
   return FA_OK;
 }
 
@@ -1308,6 +1553,52 @@ int fa_fwd_sync(const fa_problem* p, const void* q, const void* k, const void* v
   return launch(p, nullptr, q, k, v, o, ex, workspace, workspace_bytes, stream);
 }
 
+int fa_fwd_split_count(const fa_problem* p, int32_t splits, int32_t cus, int32_t* effective) {
+  if (!effective) return FA_ERR_NULL;
+  const TileConfig* tile = nullptr;
+  int rc = validate(p, &tile);
+  if (rc) return rc;
+  if (cus < 0) return FA_ERR_SPLIT;
+  int n = cus;
+  if (n == 0) {
+    rc = device_cus(&n);
+    if (rc) return rc;
+  }
+  int s = 0;
+  rc = resolve_splits(p, tile, key_layout(p, tile), splits, n, &s);
+  if (rc) return rc;
+  *effective = s;
+  return FA_OK;
+}
+
+int fa_fwd_split_workspace_bytes(const fa_problem* p, int32_t splits, uint64_t* bytes) {
+  if (!bytes) return FA_ERR_NULL;
+  const TileConfig* tile = nullptr;
+  int rc = validate(p, &tile);
+  if (rc) return rc;
+  const KeyLayout lay = key_layout(p, tile);
+  int cus = 1;   // an explicit count does not depend on the device
+  if (splits == 0) {
+    rc = device_cus(&cus);
+    if (rc) return rc;
+  }
+  int s = 0;
+  rc = resolve_splits(p, tile, lay, splits, cus, &s);
+  if (rc) return rc;
+  *bytes = s > 1 ? split_layout(p, lay, s).end : lay.workspace_bytes();
+  return FA_OK;
+}
+
+int fa_fwd_split(const fa_problem* p, int32_t splits, const fa_strides* strides, const void* q,
+                 const void* k, const void* v, void* o, float* lse, void* workspace,
+                 uint64_t workspace_bytes, void* stream) {
+  Extras ex;
+  ex.lse = lse;
+  ex.split = true;
+  ex.splits = splits;
+  return launch(p, strides, q, k, v, o, ex, workspace, workspace_bytes, stream);
+}
+
 int fa_kernel_count(void) { return kNumTiles; }
 
 const char* fa_kernel_name(int32_t kernel) {
@@ -1332,6 +1623,7 @@ const char* fa_strerror(int status) {
     case FA_ERR_CAUSAL: return "unknown causal mode";
     case FA_ERR_TRACE: return "trace needs a buffer of fa_fwd_trace_count() 64-bit words";
     case FA_ERR_SCRATCH: return "problem needs more workspace than fa_fwd_noalloc's scratch (FA_NOALLOC_SCRATCH_BYTES)";
+    case FA_ERR_SPLIT: return "split count outside 0..1024 (or a negative CU count)";
     default: return "unknown status";
   }
 }

@@ -52,7 +52,8 @@ enum fa_status {
   FA_ERR_CAPTURE = 11,      /* capture stats buffer too small */
   FA_ERR_CAUSAL = 12,       /* unknown causal mode */
   FA_ERR_TRACE = 13,        /* trace buffer too small */
-  FA_ERR_SCRATCH = 14       /* fa_fwd_noalloc: workspace need above FA_NOALLOC_SCRATCH_BYTES */
+  FA_ERR_SCRATCH = 14,      /* fa_fwd_noalloc: workspace need above FA_NOALLOC_SCRATCH_BYTES */
+  FA_ERR_SPLIT = 15         /* split count outside 0..1024, or a negative CU count */
 };
 
 enum fa_acc {
@@ -261,6 +262,39 @@ const char* fa_kernel_name(int32_t kernel);
 #define FA_NOALLOC_SCRATCH_BYTES ((64ull << 20) + (64ull << 10))
 int fa_fwd_noalloc(const fa_problem* p, const void* q, const void* k, const void* v, void* o,
                    void* stream);
+
+/*
+ * Key-split forward: fa_fwd_strided() (strides may be NULL for contiguous
+ * tensors; lse may be NULL) that cuts the key range of every 256-row query
+ * tile into `splits` near-equal parts of whole key blocks, runs each
+ * (tile, part) as its own work item of the attention kernel (a separate
+ * instantiation of the same tile), and combines the parts in a second
+ * kernel: each part writes its rows' O normalised by the part's own row sum
+ * (FP32) and its log-sum-exp lse_s, and the merge forms
+ * O = sum_s exp(lse_s - M) O_s / sum_s exp(lse_s - M), M = max_s lse_s,
+ * lse = M + ln sum_s exp(lse_s - M). For problems with fewer query tiles
+ * than the GPU has CUs (short query ranges, small batch against long keys)
+ * this keeps every CU busy; fa_fwd() runs one work item per tile and leaves
+ * the rest idle. The results equal fa_fwd_lse()'s up to FP32 summation order
+ * (FP16 accumulator: each part rounds its own 512-key packets). splits = 0
+ * picks the count automatically on the current device (fa_fwd_split_count),
+ * n >= 1 is clamped to the key blocks of the tile, and a count of 1 is
+ * exactly fa_fwd_lse(). Workspace: fa_fwd_split_workspace_bytes(), which
+ * adds (4 + 512) * splits bytes per query row to fa_fwd_workspace_bytes().
+ * The reference has no counterpart: its task split covers (batch * head,
+ * query block) only (K32/cce_task.h:28-35); this is the single-GPU form of
+ * a key-sharded forward, whose per-shard (O, lse) pairs merge the same way.
+ */
+int fa_fwd_split_count(const fa_problem* p, int32_t splits, int32_t cus, int32_t* effective);
+int fa_fwd_split_workspace_bytes(const fa_problem* p, int32_t splits, uint64_t* bytes);
+int fa_fwd_split(const fa_problem* p, int32_t splits, const fa_strides* strides, const void* q,
+                 const void* k, const void* v, void* o, float* lse, void* workspace,
+                 uint64_t workspace_bytes, void* stream);
+/* fa_fwd_split_count: the effective part count for a requested one (0 =
+ * automatic) on a GPU with `cus` compute units (0 = the current device's):
+ * the automatic choice models the launch's duration per candidate count
+ * (work items per CU, per-item overhead, the merge's HBM traffic) and splits
+ * only when that beats one pass over the keys by 10 %. */
 
 /* Static message for a status code. */
 const char* fa_strerror(int status);

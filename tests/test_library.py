@@ -262,3 +262,92 @@ def test_noalloc_rejects_before_touching_the_gpu(lib):
     # The headline configuration (B=2, Nk=131072, no key tail) fits.
     rc, size = ws_bytes(lib, problem(batch=2, seq_q=131072, seq_k=131072))
     assert rc == 0 and size <= binding.NOALLOC_SCRATCH_BYTES
+
+
+def split_count(lib, prob, splits, cus=256):
+    n = C.c_int32(-1)
+    rc = lib.fa_fwd_split_count(C.byref(prob), splits, cus, C.byref(n))
+    return rc, n.value
+
+
+def split_ws(lib, prob, splits):
+    size = C.c_uint64(0)
+    rc = lib.fa_fwd_split_workspace_bytes(C.byref(prob), splits, C.byref(size))
+    return rc, size.value
+
+
+def test_split_count_choice(lib):
+    # Automatic choice on a 256-CU GPU: grids with at least 2 x 256 tiles are
+    # never split; 12 query tiles against 131072 keys are; c0 (192 tiles of
+    # 32 key blocks, one round) gains too little from splitting to pay for
+    # the merge.
+    assert split_count(lib, problem(batch=2, seq_q=131072, seq_k=131072), 0) == (0, 1)
+    assert split_count(lib, problem(seq_q=4096, seq_k=4096), 0) == (0, 1)
+    rc, n = split_count(lib, problem(seq_q=256, seq_k=131072), 0)
+    assert rc == 0 and 16 <= n <= 64, n
+    # Causal masks: the choice looks at the key blocks each tile sees. One
+    # bottom-right query tile at the end of 131072 keys sees them all and is
+    # split; the causal headline shape has tiles enough.
+    rc, n = split_count(lib, problem(seq_q=256, seq_k=131072, causal=2), 0)
+    assert rc == 0 and n > 1
+    assert split_count(lib, problem(batch=2, seq_q=131072, seq_k=131072, causal=1), 0) == (0, 1)
+    # Top-left, Nq = Nk = 1024 on 4 CUs: 4 tiles of 2, 4, 6 and 8 blocks. The
+    # 8-block tile alone bounds the launch at 9.5 block times; two parts per
+    # tile (blocks 0-3, 4-7) bring it to ~7.3 with the merge, so 2 is taken.
+    assert split_count(lib, problem(heads_q=1, seq_q=1024, seq_k=1024, causal=1), 0, cus=4) == (0, 2)
+    # Full attention: the modelled best count. 24 tiles of 512 key blocks on
+    # 256 CUs: 10 parts are 240 items in one round of 51.2 + 1.5 block
+    # times; 11 would need a second round.
+    assert split_count(lib, problem(seq_q=512, seq_k=65536), 0) == (0, 10)
+    # Explicit counts are clamped to the key blocks (128-key tile: 1000 keys
+    # are 8 blocks) and do not depend on the CU count.
+    assert split_count(lib, problem(seq_k=1000), 100) == (0, 8)
+    assert split_count(lib, problem(seq_k=1000), 3, cus=1) == (0, 3)
+    assert split_count(lib, problem(seq_k=1000), 1) == (0, 1)
+    # Errors: counts outside 0..1024, a negative CU count, bad geometry.
+    assert split_count(lib, problem(), -1)[0] == 15
+    assert split_count(lib, problem(), 1025)[0] == 15
+    assert split_count(lib, problem(), 2, cus=-1)[0] == 15
+    assert split_count(lib, problem(dim=64), 2)[0] == 3
+    assert lib.fa_fwd_split_count(C.byref(problem()), 2, 256, None) == 1
+
+
+def test_split_workspace(lib):
+    # One part: fa_fwd_workspace_bytes. n parts add the parts' lse (FP32
+    # [n][R], padded to 256 bytes) and O (FP32 [n][R][128]), R = B * Hq * Nq.
+    prob = problem(batch=1, heads_q=12, seq_q=300, seq_k=4096)
+    _, base = ws_bytes(lib, prob)
+    assert split_ws(lib, prob, 1) == (0, base)
+    rows = 12 * 300
+    for n in (2, 5, 32):
+        lp = (n * rows * 4 + 255) // 256 * 256
+        assert split_ws(lib, prob, n) == (0, base + lp + n * rows * 128 * 4)
+    # Clamped like the count: 4096 keys are 32 blocks of 128.
+    assert split_ws(lib, prob, 100) == split_ws(lib, prob, 32)
+    assert split_ws(lib, prob, -3)[0] == 15
+    assert lib.fa_fwd_split_workspace_bytes(C.byref(prob), 2, None) == 1
+
+
+def test_split_rejects_before_launch(lib):
+    prob = problem(seq_q=256, seq_k=8192)
+    p = C.c_void_p(4096)
+    _, size = split_ws(lib, prob, 4)
+    assert lib.fa_fwd_split(C.byref(prob), 4, None, None, p, p, p, None, p, size, None) == 1
+    assert lib.fa_fwd_split(C.byref(prob), 4, None, p, p, p, p, None, p, size - 1, None) == 6
+    assert lib.fa_fwd_split(C.byref(prob), 4, None, p, p, p, p, C.c_void_p(4100), p, size,
+                            None) == 5
+    assert lib.fa_fwd_split(C.byref(prob), -1, None, p, p, p, p, None, p, size, None) == 15
+    assert lib.fa_fwd_split(C.byref(problem(dim=64)), 4, None, p, p, p, p, None, p, size,
+                            None) == 3
+    bad = binding.FaStrides()
+    for name in ("q", "k", "v", "o"):
+        getattr(bad, name)[:] = (256 * 128, 256 * 128, 132)
+    assert lib.fa_fwd_split(C.byref(prob), 4, C.byref(bad), p, p, p, p, None, p, size,
+                            None) == 5
+    # The binding's configuration checks.
+    assert binding.AttentionConfig(splits=0).splits == 0
+    for bad_cfg in ({"splits": -1}, {"splits": 1025}, {"splits": 2.0}, {"splits": True},
+                    {"splits": 2, "sync": True}, {"splits": 2, "capture": True},
+                    {"splits": 0, "trace": True}):
+        with pytest.raises(ValueError):
+            binding.AttentionConfig(**bad_cfg)

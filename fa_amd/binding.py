@@ -168,6 +168,8 @@ class Operator:
         self.lib = load_library(library) if not isinstance(library, C.CDLL) else library
         self.workspace = None
         self.buffers = {}
+        self.plans = {}          # (shapes, scale, device) -> (FaProblem, workspace bytes)
+        self.tiles = {}          # (q shape, k shape) -> (rows, keys) granularity
         self.last = None
 
     def message(self, status):
@@ -180,10 +182,13 @@ class Operator:
 
     def tile(self, q_shape, k_shape):
         """(query rows, keys) granularity of the kernel the library would use."""
-        prob = make_problem(q_shape, k_shape, 1.0, self.config)
-        rows, keys = C.c_int32(), C.c_int32()
-        self.check(self.lib.fa_fwd_tile(C.byref(prob), C.byref(rows), C.byref(keys)), "tile")
-        return rows.value, keys.value
+        key = (tuple(q_shape), tuple(k_shape))
+        if key not in self.tiles:
+            prob = make_problem(q_shape, k_shape, 1.0, self.config)
+            rows, keys = C.c_int32(), C.c_int32()
+            self.check(self.lib.fa_fwd_tile(C.byref(prob), C.byref(rows), C.byref(keys)), "tile")
+            self.tiles[key] = (rows.value, keys.value)
+        return self.tiles[key]
 
     def kernel(self, q_shape, k_shape):
         """1-based tile configuration the library would launch (automatic choice resolved)."""
@@ -285,15 +290,22 @@ class Operator:
         scale = q.shape[3] ** -0.5 if scale is None else float(scale)
         if not (scale > 0 and math.isfinite(scale)):
             raise ValueError("scale must be finite and positive")
-        prob = make_problem(q.shape, k.shape, scale, self.config)
-        size = C.c_uint64()
         splits = self.config.splits
-        if splits is None:
-            self.check(self.lib.fa_fwd_workspace_bytes(C.byref(prob), C.byref(size)), "prepare")
-        else:
-            with torch.cuda.device(q.device):
-                self.check(self.lib.fa_fwd_split_workspace_bytes(C.byref(prob), splits,
-                                                                 C.byref(size)), "prepare")
+        # The problem and its workspace size depend on the shapes, the scale
+        # and (automatic split count) the device only: computed once each.
+        plan_key = (tuple(q.shape), tuple(k.shape), scale, q.device)
+        if plan_key not in self.plans:
+            prob = make_problem(q.shape, k.shape, scale, self.config)
+            size = C.c_uint64()
+            if splits is None:
+                self.check(self.lib.fa_fwd_workspace_bytes(C.byref(prob), C.byref(size)),
+                           "prepare")
+            else:
+                with torch.cuda.device(q.device):
+                    self.check(self.lib.fa_fwd_split_workspace_bytes(C.byref(prob), splits,
+                                                                     C.byref(size)), "prepare")
+            self.plans[plan_key] = (prob, size.value)
+        prob, size = self.plans[plan_key]
         out = self.buffers_for(q, k)
         capture = self.config.capture
         lse = self.buffers_for(q, k, lse=True) if (return_lse or capture) else None
@@ -303,7 +315,7 @@ class Operator:
         if strided and (capture or trace is not None or self.config.sync):
             raise ValueError("capture, trace and sync modes need contiguous Q/K/V")
         with torch.cuda.device(q.device):
-            need = max(size.value, 16)
+            need = max(size, 16)
             if self.workspace is None or self.workspace.device != q.device \
                     or self.workspace.numel() < need:
                 self.workspace = torch.empty(need, dtype=torch.uint8, device=q.device)

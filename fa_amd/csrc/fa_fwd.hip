@@ -114,7 +114,7 @@ constexpr int TRACE_WORDS = 8;
 // instead of o and lse, each part's O normalised by its own row sum into
 // opart (FP32 [splits][B * Hq * Nq][128]) and the part's natural-log
 // log-sum-exp into lpart (FP32 [splits][B * Hq * Nq]; -inf for a part in
-// which the row sees no key, whose opart row is left unwritten).
+// which the row sees no key, whose opart row then holds zeros).
 struct Strides {
   int64_t b, h, n;   // batch, head and row strides in elements; the 128 dims are contiguous
 };
@@ -240,11 +240,25 @@ __global__ void __launch_bounds__(256) fa_poison_kernel(u32x4* p, uint64_t n16) 
 //   O = sum_s w_s O_s / sum_s w_s,  lse = M + ln sum_s w_s,
 //   w_s = exp(lse_s - M),  M = max_s lse_s,
 // the log-sum-exp algebra of the online softmax applied once across parts.
-// A part whose lse is -inf (the row sees none of its keys) has no weight and
-// its O row is not read; a row that sees no key at all gets O = 0 and
-// lse = -inf. 32 lanes per row (4 of the 128 dims each), 8 rows per
-// 256-thread block, grid-stride over the rows = B * Hq * Nq; o is written
-// through its strides, lse (may be null) contiguously.
+// A part whose lse is -inf (the row sees none of its keys) has weight 0 (its
+// O row holds zeros); a row that sees no key at all gets O = 0 and
+// lse = -inf. 32 lanes per row: lane i reads the lse of parts i, i + 32, ...,
+// so the maximum and the weight sum are reductions over the 32 lanes, and
+// each lane accumulates 4 of the 128 dims over all parts, with the weights
+// broadcast from the lane that computed them and the O loads independent of
+// each other (unrolled, so several are in flight). 8 rows per 256-thread
+// block, grid-stride over the rows = B * Hq * Nq; o is written through its
+// strides, lse (may be null) contiguously.
+__device__ __forceinline__ float max32(float x) {
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 32));
+  return x;
+}
+__device__ __forceinline__ float sum32(float x) {
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) x += __shfl_xor(x, m, 32);
+  return x;
+}
 __global__ void __launch_bounds__(256) fa_merge_kernel(const float* __restrict__ opart,
                                                        const float* __restrict__ lpart,
                                                        _Float16* __restrict__ o,
@@ -255,20 +269,37 @@ __global__ void __launch_bounds__(256) fa_merge_kernel(const float* __restrict__
   const int64_t step = (int64_t)gridDim.x * 8;
   for (int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5); row < rows; row += step) {
     float mx = -INFINITY;
-    for (int s = 0; s < splits; ++s) mx = fmaxf(mx, lpart[s * rows + row]);
+    for (int s = sub; s < splits; s += 32) mx = fmaxf(mx, lpart[s * rows + row]);
+    mx = max32(mx);
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, wsum = 0.f;
     if (mx != -INFINITY) {
-      for (int s = 0; s < splits; ++s) {
-        const float ls = lpart[s * rows + row];
-        if (ls == -INFINITY) continue;
-        const float w = __builtin_amdgcn_exp2f((ls - mx) * (float)LOG2E);
-        const float4 v = *reinterpret_cast<const float4*>(opart + ((size_t)s * rows + row) * HD + 4 * sub);
-        a0 = __builtin_fmaf(w, v.x, a0);
-        a1 = __builtin_fmaf(w, v.y, a1);
-        a2 = __builtin_fmaf(w, v.z, a2);
-        a3 = __builtin_fmaf(w, v.w, a3);
+      const float* col = opart + (size_t)row * HD + 4 * sub;
+      const size_t pstride = (size_t)rows * HD;
+      for (int s0 = 0; s0 < splits; s0 += 32) {
+        const int s = s0 + sub;
+        const float ls = s < splits ? lpart[s * rows + row] : -INFINITY;
+        const float w = ls == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((ls - mx) * (float)LOG2E);
         wsum += w;
+        const int n = min(32, splits - s0);
+        auto add = [&](float wi, const float4& v) {
+          a0 = __builtin_fmaf(wi, v.x, a0);
+          a1 = __builtin_fmaf(wi, v.y, a1);
+          a2 = __builtin_fmaf(wi, v.z, a2);
+          a3 = __builtin_fmaf(wi, v.w, a3);
+        };
+        int i = 0;
+        for (; i + 4 <= n; i += 4) {        // four loads in flight before their FMAs
+          float4 v[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            v[j] = *reinterpret_cast<const float4*>(col + (size_t)(s0 + i + j) * pstride);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) add(__shfl(w, i + j, 32), v[j]);
+        }
+        for (; i < n; ++i)
+          add(__shfl(w, i, 32), *reinterpret_cast<const float4*>(col + (size_t)(s0 + i) * pstride));
       }
+      wsum = sum32(wsum);
     }
     const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
     const int64_t bh = row / seq_q;
@@ -456,7 +487,14 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
     if constexpr (TRACE) trace_record(args, tile, real0, clk0, 0, BN);
     if (!row_ok) return;
     if constexpr (SPLIT) {
+      // The part's lse is -inf and its O row zeros (weight 0 in the merge).
       if (hf == 0) args.lpart[part] = -INFINITY;
+      float* prow = args.opart + part * HD;
+      const float4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) *reinterpret_cast<float4*>(prow + dt * 32 + 8 * g + 4 * hf) = zero;
       return;
     }
     if (args.lse && hf == 0) args.lse[grow] = -INFINITY;

@@ -136,3 +136,17 @@ def test_algorithmic_bytes_of_every_configuration():
     for case in CASES:
         assert traffic.algorithmic_bytes(case) == 2 * case.batch * (case.heads_q + case.heads_kv) \
             * case.seq_len * case.dim * 2
+
+
+def test_split_table_render():
+    from fa_amd.measure import split
+
+    assert split.parse_shape("1,12,1,256,131072") == (1, 12, 1, 256, 131072)
+    with pytest.raises(Exception):
+        split.parse_shape("1,12,1")
+    rows = [{"shape": (1, 12, 1, 256, 131072), "parts": 21, "one_us": 2149.0, "split_us": 224.0,
+             "one_tflops": 95.9, "split_tflops": 920.3, "max_diff": 1.2e-4}]
+    lines = split.render(rows, "fp32", "python -m fa_amd.measure.split")
+    assert lines[1] == "command: python -m fa_amd.measure.split"
+    row = lines[3].split()
+    assert row[:3] == ["1,12,1,256,131072", "12", "21"] and row[7] == "9.59x"

@@ -13,7 +13,9 @@
 // are masked, the per-row log-sum-exp is written on request, and an optional
 // causal mask makes a tile stream only the key blocks up to its diagonal.
 // Separate instantiations add the capture (per-block softmax statistics),
-// trace (per-tile clock stamps) and synchronous debug modes.
+// trace (per-tile clock stamps) and synchronous debug modes, and the
+// key-split mode: work items are (tile, part of its key range), whose
+// partial results a merge kernel combines through their log-sum-exp.
 //
 // Matrix products run transposed so the softmax is lane-local:
 //   S^T = K Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS, B = Q^T

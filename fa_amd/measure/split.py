@@ -8,9 +8,11 @@ forward (``fa_fwd_split``) cuts every tile's key range into parts, runs each
 each shape this prints the library's automatic part count, the device time
 per forward of both paths (HIP events around ``--steps`` forwards after
 ``--warmup``), the achieved QK/PV TFLOP/s (4 B Hq Nq Nk 128 FLOP) and the
-largest difference between the two outputs.
+largest difference between the two outputs. With ``--sweep`` it times the
+split forward at every explicit part count of SWEEP_COUNTS instead, to check
+the automatic choice against the fastest count.
 
-Usage: python -m fa_amd.measure.split [--acc fp32|fp16] [--shape B,Hq,Hkv,Nq,Nk ...]
+Usage: python -m fa_amd.measure.split [--acc fp32|fp16] [--sweep] [--shape B,Hq,Hkv,Nq,Nk ...]
 """
 
 from __future__ import annotations
@@ -30,6 +32,9 @@ SHAPES = [
     (1, 12, 1, 4096, 4096),
 ]
 PEAK_TFLOPS = 2516.6
+# Explicit part counts of the sweep (counts above a shape's key blocks are skipped).
+SWEEP_COUNTS = [1, 2, 3, 4, 5, 6, 8, 10, 12, 16, 21, 24, 32, 42, 64]
+SWEEP_SHAPES = SHAPES[1:] + [(1, 12, 1, 8192, 8192), (1, 12, 1, 2048, 32768), (1, 4, 1, 2048, 131072)]
 
 
 def parse_shape(text):
@@ -39,20 +44,26 @@ def parse_shape(text):
     return vals
 
 
-def measure(shape, acc, warmup, steps, seed=0):
+def _inputs(shape, seed):
     import torch
 
     from fa_amd import build
-    from fa_amd.binding import AttentionConfig, Operator
-    from fa_amd.harness import timing
 
     if not build.LIBRARY.is_file():
         raise FileNotFoundError(f"{build.LIBRARY} is not built (python -m fa_amd.build)")
     b, hq, hkv, nq, nk = shape
     g = torch.Generator().manual_seed(seed)
-    q = torch.randn(b, hq, nq, 128, generator=g, dtype=torch.float16).cuda()
-    k = torch.randn(b, hkv, nk, 128, generator=g, dtype=torch.float16).cuda()
-    v = torch.randn(b, hkv, nk, 128, generator=g, dtype=torch.float16).cuda()
+    return tuple(torch.randn(b, h, n, 128, generator=g, dtype=torch.float16).cuda()
+                 for h, n in ((hq, nq), (hkv, nk), (hkv, nk)))
+
+
+def measure(shape, acc, warmup, steps, seed=0):
+    from fa_amd import build
+    from fa_amd.binding import AttentionConfig, Operator
+    from fa_amd.harness import timing
+
+    b, hq, hkv, nq, nk = shape
+    q, k, v = _inputs(shape, seed)
     one = Operator(build.LIBRARY, AttentionConfig(acc=acc))
     split = Operator(build.LIBRARY, AttentionConfig(acc=acc, splits=0))
     flops = 4.0 * b * hq * nq * nk * 128
@@ -65,6 +76,36 @@ def measure(shape, acc, warmup, steps, seed=0):
         "one_tflops": flops / us_one / 1e6, "split_tflops": flops / us_split / 1e6,
         "max_diff": diff,
     }
+
+
+def sweep(shape, acc, warmup, steps, seed=0):
+    """(automatic count, [(count, device us)]) over SWEEP_COUNTS."""
+    from fa_amd import build
+    from fa_amd.binding import AttentionConfig, Operator
+    from fa_amd.harness import timing
+
+    q, k, v = _inputs(shape, seed)
+    auto = Operator(build.LIBRARY, AttentionConfig(acc=acc, splits=0)).split_count(q.shape, k.shape)
+    res = []
+    for n in SWEEP_COUNTS:
+        if n > -(-shape[4] // 128):
+            continue
+        op = Operator(build.LIBRARY, AttentionConfig(acc=acc, splits=n))
+        res.append((n, timing.device_us(lambda: op(q, k, v), iters=steps, warmup=warmup)))
+    return auto, res
+
+
+def render_sweep(rows, acc, command):
+    lines = [f"# key-split forward, hip_fa_{acc}acc: device us per forward at each explicit part count,",
+             "# against the library's automatic count (one MI355X)",
+             f"command: {command}"]
+    for shape, auto, res in rows:
+        times = dict(res)
+        best = min(res, key=lambda r: r[1])
+        lines.append(f"{','.join(map(str, shape))}: automatic {auto} ({times[auto]:.0f} us), fastest "
+                     f"{best[0]} ({best[1]:.0f} us, automatic at {times[auto] / best[1]:.3f}x)")
+        lines.append("  " + " ".join(f"{n}:{us:.0f}" for n, us in res))
+    return lines
 
 
 def render(rows, acc, command):
@@ -86,6 +127,7 @@ def render(rows, acc, command):
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--acc", default="fp32", choices=("fp32", "fp16"))
+    ap.add_argument("--sweep", action="store_true", help="time every count of SWEEP_COUNTS")
     ap.add_argument("--shape", type=parse_shape, action="append",
                     help="B,Hq,Hkv,Nq,Nk (repeatable; default: the built-in list)")
     ap.add_argument("--warmup", type=int, default=3)
@@ -97,10 +139,14 @@ def main(argv=None) -> int:
     if repo not in sys.path:
         sys.path.insert(0, repo)
     rows = []
-    for shape in args.shape or SHAPES:
+    command = args.command or "python -m fa_amd.measure.split" + (" --sweep" if args.sweep else "")
+    for shape in args.shape or (SWEEP_SHAPES if args.sweep else SHAPES):
         print(f"measuring {shape}", flush=True)
-        rows.append(measure(shape, args.acc, args.warmup, args.steps))
-    lines = render(rows, args.acc, args.command or "python -m fa_amd.measure.split")
+        if args.sweep:
+            rows.append((shape,) + sweep(shape, args.acc, args.warmup, args.steps))
+        else:
+            rows.append(measure(shape, args.acc, args.warmup, args.steps))
+    lines = (render_sweep if args.sweep else render)(rows, args.acc, command)
     print("\n".join(lines), flush=True)
     if args.out:
         with open(args.out, "w", encoding="utf-8") as f:

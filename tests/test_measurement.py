@@ -150,3 +150,13 @@ def test_split_table_render():
     assert lines[1] == "command: python -m fa_amd.measure.split"
     row = lines[3].split()
     assert row[:3] == ["1,12,1,256,131072", "12", "21"] and row[7] == "9.59x"
+
+
+def test_split_sweep_render():
+    from fa_amd.measure import split
+
+    rows = [((1, 12, 1, 1024, 131072), 16, [(1, 2195.0), (5, 755.0), (16, 760.0)])]
+    lines = split.render_sweep(rows, "fp32", "python -m fa_amd.measure.split --sweep")
+    assert lines[3] == ("1,12,1,1024,131072: automatic 16 (760 us), fastest 5 (755 us, "
+                        "automatic at 1.007x)")
+    assert lines[4] == "  1:2195 5:755 16:760"

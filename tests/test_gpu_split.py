@@ -144,3 +144,26 @@ def test_split_long_keys_sampled_rows(library_path):
         got = out.float().cpu().numpy()[tuple(np.array(rows).T)]
         check(got, orc.attention_rows_f64(q, k, v, rows), acc, "split long")
         assert times["split"] < 0.5 * times["one-pass"], times
+
+
+@pytest.mark.parametrize("acc", ["fp32", "fp16"])
+@pytest.mark.parametrize("causal", ["none", "bottom_right"])
+def test_split_million_keys_sampled_rows(library_path, causal, acc):
+    """A million ragged keys (the parts' buffer offsets and ranges near their
+    32-bit limits) against 512 query rows of 4 heads (8 tiles, which the
+    automatic count cuts into 32 parts each), sampled rows against the
+    float64 oracle."""
+    nq, nk = 512, 1_048_573
+    say(f"case split million keys nq={nq} nk={nk} causal={causal} acc={acc}: generating inputs")
+    q, k, v = make(1, 4, 1, nq, nk, seed=nk % 1000 + nq)
+    op = Operator(library_path, AttentionConfig(acc=acc, causal=causal, splits=0))
+    say(f"  parts per tile: {op.split_count(q.shape, k.shape)}")
+    out, lse = op(q.cuda(), k.cuda(), v.cuda(), return_lse=True)
+    torch.cuda.synchronize()
+    rows = orc.sample_rows(q.shape, 24, seed=nq + nk)
+    idx = torch.tensor(rows)
+    got = out[idx[:, 0], idx[:, 1], idx[:, 2]].float().cpu().numpy()
+    check(got, orc.attention_rows_f64(q, k, v, rows, causal=causal), acc, "split million keys",
+          orc.attention_rows_f64(q, k, v.abs(), rows, causal=causal))
+    check_lse(lse[idx[:, 0], idx[:, 1], idx[:, 2]].cpu().numpy(),
+              orc.lse_rows_f64(q, k, rows, causal=causal), "split million keys")

@@ -167,3 +167,33 @@ def test_split_million_keys_sampled_rows(library_path, causal, acc):
           orc.attention_rows_f64(q, k, v.abs(), rows, causal=causal))
     check_lse(lse[idx[:, 0], idx[:, 1], idx[:, 2]].cpu().numpy(),
               orc.lse_rows_f64(q, k, rows, causal=causal), "split million keys")
+
+
+def test_split_graph_capture_replays(library_path):
+    """fa_fwd_split captured in a HIP graph (three kernels, no memset): every
+    replay, with eager work and synchronisation in between and the inputs
+    changed in place, equals the eager split forward for the current inputs."""
+    say("case split graph capture B1 Hq12 nq=256 nk=8192 splits=6")
+    g = torch.Generator().manual_seed(23)
+    q = torch.randn(1, 12, 256, 128, generator=g, dtype=torch.float16).cuda()
+    k = torch.randn(1, 1, 8192, 128, generator=g, dtype=torch.float16).cuda()
+    v = torch.randn(1, 1, 8192, 128, generator=g, dtype=torch.float16).cuda()
+    op = Operator(library_path, AttentionConfig(splits=6))
+    op(q, k, v, return_lse=True)                  # allocates the cached outputs and workspace
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            out, lse = op(q, k, v, return_lse=True)
+    torch.cuda.synchronize()
+    eager = Operator(library_path, AttentionConfig(splits=6))
+    for rep in range(4):
+        q.copy_(torch.randn(q.shape, generator=g, dtype=torch.float16).cuda())
+        v.mul_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want, want_lse = eager(q, k, v, return_lse=True)
+        torch.cuda.synchronize()
+        assert bool(torch.equal(out, want)) and bool(torch.equal(lse, want_lse)), rep

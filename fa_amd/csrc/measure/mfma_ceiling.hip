@@ -1,7 +1,8 @@
 // Sustained dense FP16 MFMA rate of the board: a measurement kernel, not part
-// of the attention library. It shares the attention kernel's launch shape
-// (8 waves of 64 lanes per workgroup, two waves per SIMD, one workgroup per
-// CU at a time) and its matrix instruction (v_mfma_f32_32x32x16_f16), and
+// of the attention library. Modes 0-4 share the attention kernel's launch
+// shape (8 waves of 64 lanes per workgroup, two waves per SIMD), modes 5-6
+// run one wave per SIMD; all use its matrix instruction
+// (v_mfma_f32_32x32x16_f16), and
 // does nothing but issue those instructions for a fixed number of
 // iterations, so its rate is what the matrix cores sustain on this board
 // under its power limit when nothing else runs beside them.
@@ -23,6 +24,13 @@
 //   MODE 4  both operands of every MFMA read from LDS (2 KiB per MFMA and
 //           wave, twice the attention kernel's traffic): how close LDS
 //           bandwidth comes to limiting the matrix pipe.
+//   MODE 5  one wave per SIMD (4 waves per workgroup, up to 512 registers
+//           per lane), each A operand read from LDS feeding two MFMAs, eight
+//           reads in flight: the issue rate of the single-wave layout a tile
+//           of 64 query rows per wave would need.
+//   MODE 6  mode 5 plus, after every MFMA, the same VALU mix as mode 2 in
+//           the same wave: a 64-row-per-wave softmax overlapped with its own
+//           matrix work, without dependencies.
 //
 // Operands are FP16 values supplied by the caller (random normal data, so the
 // datapath toggles as it does on real inputs). Every wave keeps four
@@ -41,7 +49,8 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 512;
+constexpr int kThreads = 512;         // two waves per SIMD (modes 0-4)
+constexpr int kThreadsSingle = 256;   // one wave per SIMD (modes 5, 6)
 constexpr int kOperandHalves = 8192;   // 16 KiB of FP16 operands
 constexpr int kTraceWords = 8;
 constexpr int kMfmaPerIter = 16;
@@ -50,15 +59,15 @@ __device__ __forceinline__ f32x16 mfma32(h8 a, h8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <int MODE>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-fa_mfma_ceiling_kernel(const _Float16* __restrict__ operands, float* __restrict__ out,
-                       uint64_t* __restrict__ trace, int iters) {
+template <int MODE, int NT>
+__device__ __forceinline__ void ceiling_body(const _Float16* __restrict__ operands,
+                                             float* __restrict__ out, uint64_t* __restrict__ trace,
+                                             int iters) {
   const uint64_t real0 = __builtin_amdgcn_s_memrealtime();
   const uint64_t clk0 = __builtin_amdgcn_s_memtime();
   __shared__ __attribute__((aligned(16))) _Float16 lds[kOperandHalves];
   const int tid = threadIdx.x, lane = tid & 63;
-  for (int i = tid; i < kOperandHalves / 8; i += kThreads)
+  for (int i = tid; i < kOperandHalves / 8; i += NT)
     reinterpret_cast<h8*>(lds)[i] = reinterpret_cast<const h8*>(operands)[i];
   h8 a[4], b[4];
 #pragma unroll
@@ -76,10 +85,42 @@ fa_mfma_ceiling_kernel(const _Float16* __restrict__ operands, float* __restrict_
   // LDS operand address of MFMA n of an iteration: 16 B per lane, 1 KiB per
   // MFMA, cycling through the 16 KiB buffer (distinct lanes, distinct banks).
   const char* base = reinterpret_cast<const char*>(lds) + lane * 16;
+  // Modes 5 and 6: the eight operand fragments of the first iteration, read
+  // in the order the loop reads them, so the compiler's wait counts stay the
+  // same from one iteration to the next and no iteration drains the reads.
+  h8 fr8[kMfmaPerIter / 2];
+  if constexpr (MODE == 5 || MODE == 6) {
+#pragma unroll
+    for (int f = 0; f < kMfmaPerIter / 2; ++f) {
+      fr8[f] = *reinterpret_cast<const h8*>(base + f * 1024);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
   for (int it = 0; it < iters; ++it) {
     if constexpr (MODE == 0) {
 #pragma unroll
       for (int n = 0; n < kMfmaPerIter; ++n) acc[n & 3] = mfma32(a[n >> 2], b[n & 3], acc[n & 3]);
+    } else if constexpr (MODE == 5 || MODE == 6) {
+      // Eight reads in flight across iterations: operand f of an iteration
+      // is read while the previous iteration's operand f feeds its MFMAs
+      // (the addresses repeat every iteration), so a single wave never
+      // waits for LDS at an iteration boundary.
+#pragma unroll
+      for (int f = 0; f < kMfmaPerIter / 2; ++f) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int n = 2 * f + u;
+          acc[n & 3] = mfma32(fr8[f], b[u], acc[n & 3]);
+          if constexpr (MODE == 6) {
+            w[n] = __builtin_amdgcn_exp2f(w[n]) * 0.5f;
+            w[(n + 5) & 15] = __builtin_fmaf(w[(n + 5) & 15], 0.999f, -0.001f);
+            w[(n + 11) & 15] = __builtin_fmaf(w[(n + 11) & 15], 0.999f, -0.001f);
+          }
+        }
+        // Read after the fragment's last use, into the same registers.
+        fr8[f] = *reinterpret_cast<const h8*>(base + f * 1024);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     } else if constexpr (MODE == 4) {
       h8 fa[4], fb[4];
 #pragma unroll
@@ -132,11 +173,11 @@ fa_mfma_ceiling_kernel(const _Float16* __restrict__ operands, float* __restrict_
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) sum += acc[j][r];
-  if constexpr (MODE == 2) {
+  if constexpr (MODE == 2 || MODE == 6) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) sum += w[j];
   }
-  out[(size_t)blockIdx.x * kThreads + tid] = sum;
+  out[(size_t)blockIdx.x * NT + tid] = sum;
   if (trace) {
     const uint64_t real1 = __builtin_amdgcn_s_memrealtime();
     const uint64_t clk1 = __builtin_amdgcn_s_memtime();
@@ -154,23 +195,52 @@ fa_mfma_ceiling_kernel(const _Float16* __restrict__ operands, float* __restrict_
   }
 }
 
+template <int MODE>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+fa_mfma_ceiling_kernel(const _Float16* __restrict__ operands, float* __restrict__ out,
+                       uint64_t* __restrict__ trace, int iters) {
+  ceiling_body<MODE, kThreads>(operands, out, trace, iters);
+}
+
+template <int MODE>
+__global__ void __launch_bounds__(kThreadsSingle) __attribute__((amdgpu_waves_per_eu(1, 1)))
+fa_mfma_ceiling_single_kernel(const _Float16* __restrict__ operands, float* __restrict__ out,
+                              uint64_t* __restrict__ trace, int iters) {
+  ceiling_body<MODE, kThreadsSingle>(operands, out, trace, iters);
+}
+
+constexpr int kModes = 7;
+int threads_of(int mode) { return mode >= 5 ? kThreadsSingle : kThreads; }
+
 }  // namespace
 
 extern "C" {
 
-// FP16 FLOPs one workgroup performs: 8 waves x iters x 16 MFMAs x 32x32x16x2.
+// FP16 FLOPs one workgroup performs in modes 0-4: 8 waves x iters x 16
+// MFMAs x 32x32x16x2.
 uint64_t fa_ceiling_flops_per_workgroup(int iters) {
   return (uint64_t)(kThreads / 64) * (uint64_t)iters * kMfmaPerIter * 32 * 32 * 16 * 2;
 }
 
+// Threads per workgroup of a mode (512, or 256 for the one-wave-per-SIMD
+// modes 5 and 6; 0 for an unknown mode) and the FP16 FLOPs one workgroup
+// performs in it.
+int fa_ceiling_threads(int mode) { return mode < 0 || mode >= kModes ? 0 : threads_of(mode); }
+uint64_t fa_ceiling_flops(int mode, int iters) {
+  return (uint64_t)(fa_ceiling_threads(mode) / 64) * (uint64_t)iters * kMfmaPerIter * 32 * 32 *
+         16 * 2;
+}
+
 // Launch the ceiling kernel: mode 0 (register operands), 1 (LDS-fed A
 // operand), 2 (LDS-fed A operand and the softmax's VALU mix), 3 (one LDS
-// read per two MFMAs) or 4 (both operands from LDS); operands = 8192 FP16 values (16-byte aligned), out = workgroups
-// x 512 floats, trace = workgroups x 8 words or NULL. Returns 0, or 1 for
-// bad arguments, 2 when the launch is rejected.
+// read per two MFMAs), 4 (both operands from LDS), 5 (one wave per SIMD,
+// one LDS read per two MFMAs) or 6 (mode 5 and the VALU mix); operands = 8192 FP16 values
+// (16-byte aligned), out = workgroups x fa_ceiling_threads(mode) floats,
+// trace = workgroups x 8 words or NULL. Returns 0, or 1 for bad arguments,
+// 2 when the launch is rejected.
 int fa_ceiling_mfma(int mode, int workgroups, int iters, const void* operands, float* out,
                     uint64_t* trace, void* stream) {
-  if (mode < 0 || mode > 4 || workgroups <= 0 || iters <= 0 || !operands || !out) return 1;
+  if (mode < 0 || mode >= kModes || workgroups <= 0 || iters <= 0 || !operands || !out) return 1;
   if ((reinterpret_cast<uintptr_t>(operands) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(trace)) & 15)
     return 1;
@@ -180,10 +250,13 @@ int fa_ceiling_mfma(int mode, int workgroups, int iters, const void* operands, f
                        reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<1>),
                        reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<2>),
                        reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<3>),
-                       reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<4>)};
+                       reinterpret_cast<const void*>(&fa_mfma_ceiling_kernel<4>),
+                       reinterpret_cast<const void*>(&fa_mfma_ceiling_single_kernel<5>),
+                       reinterpret_cast<const void*>(&fa_mfma_ceiling_single_kernel<6>)};
+  static_assert(sizeof(fns) / sizeof(fns[0]) == kModes, "one kernel per mode");
   const void* fn = fns[mode];
-  return hipLaunchKernel(fn, dim3((unsigned)workgroups), dim3(kThreads), args, 0,
-                         static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : 2;
+  return hipLaunchKernel(fn, dim3((unsigned)workgroups), dim3((unsigned)threads_of(mode)), args,
+                         0, static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : 2;
 }
 
 }  // extern "C"

@@ -12,8 +12,10 @@ current stream after warmup launches:
   and three other FP32 operations, independent of the MFMAs -- the forward's
   work without its dependencies and barriers), or with each LDS read
   feeding two MFMAs (mode 3: half the LDS traffic), or with both operands
-  read from LDS (mode 4: twice the traffic, a test of LDS bandwidth). Its
-  trace records give the clock it ran at.
+  read from LDS (mode 4: twice the traffic, a test of LDS bandwidth), or
+  with one wave per SIMD and each LDS read feeding two MFMAs, alone (mode
+  5) or with the softmax's VALU mix in the same wave (mode 6): the
+  single-wave layout a 64-row-per-wave tile would need. Its trace records give the clock it ran at.
 * ``gemm`` -- torch's FP16 matrix product (hipBLASLt) on large square and
   rectangular shapes, the rate a tuned vendor GEMM reaches.
 
@@ -36,7 +38,13 @@ import sys
 GEMM_SHAPES = ((8192, 8192, 8192), (8192, 8192, 16384), (16384, 16384, 8192))
 # MFMA loop modes of libfa_ceiling.so and their labels in measure()'s result.
 MODES = ((0, "registers"), (1, "lds_operand"), (2, "lds_operand_softmax_valu"),
-         (3, "lds_operand_read_per_two"), (4, "both_operands_lds"))
+         (3, "lds_operand_read_per_two"), (4, "both_operands_lds"),
+         (5, "one_wave_read_per_two"), (6, "one_wave_read_per_two_softmax_valu"))
+MODE_TITLES = {0: "operands in registers", 1: "A operand read from LDS",
+               2: "A operand from LDS + the softmax's VALU mix",
+               3: "one LDS operand read per two MFMAs", 4: "both operands read from LDS",
+               5: "one wave per SIMD, one LDS read per two MFMAs",
+               6: "one wave per SIMD, one LDS read per two MFMAs + the VALU mix in-wave"}
 
 
 def _library():
@@ -45,6 +53,10 @@ def _library():
     lib = C.CDLL(str(build.CEILING.library), mode=C.RTLD_LOCAL)
     lib.fa_ceiling_flops_per_workgroup.restype = C.c_uint64
     lib.fa_ceiling_flops_per_workgroup.argtypes = [C.c_int]
+    lib.fa_ceiling_threads.restype = C.c_int
+    lib.fa_ceiling_threads.argtypes = [C.c_int]
+    lib.fa_ceiling_flops.restype = C.c_uint64
+    lib.fa_ceiling_flops.argtypes = [C.c_int, C.c_int]
     lib.fa_ceiling_mfma.restype = C.c_int
     lib.fa_ceiling_mfma.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p,
                                     C.c_void_p, C.c_void_p]
@@ -58,7 +70,10 @@ def mfma_loop(mode, workgroups=2048, iters=16384, reps=3, warmup=2):
     lib = _library()
     g = torch.Generator().manual_seed(7)
     operands = torch.randn(8192, generator=g).half().cuda()
-    out = torch.empty(workgroups * 512, dtype=torch.float32, device="cuda")
+    threads = lib.fa_ceiling_threads(mode)
+    if threads <= 0:
+        raise ValueError(f"unknown MFMA loop mode {mode}")
+    out = torch.empty(workgroups * threads, dtype=torch.float32, device="cuda")
     trace = torch.zeros(workgroups, 8, dtype=torch.int64, device="cuda")
     stream = torch.cuda.current_stream()
 
@@ -83,7 +98,7 @@ def mfma_loop(mode, workgroups=2048, iters=16384, reps=3, warmup=2):
     torch.cuda.synchronize()
     if not torch.isfinite(out).all():
         raise RuntimeError("MFMA ceiling kernel produced non-finite sums")
-    flops = lib.fa_ceiling_flops_per_workgroup(iters) * workgroups
+    flops = lib.fa_ceiling_flops(mode, iters) * workgroups
     return flops / seconds / 1e12, trace.cpu().numpy()
 
 
@@ -132,6 +147,9 @@ def main(argv=None) -> int:
     ap.add_argument("--out")
     ap.add_argument("--command", default="")
     ap.add_argument("--records", help="save the loop's trace records as <prefix>_mode<m>.npy")
+    ap.add_argument("--no-gemm", action="store_true",
+                    help="run only the MFMA loops (no vendor GEMM before them)")
+    ap.add_argument("--modes", help="comma-separated loop modes (default: all)")
     args = ap.parse_args(argv)
     repo = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     if repo not in sys.path:
@@ -140,14 +158,13 @@ def main(argv=None) -> int:
 
     lines = ["# sustained dense FP16 matrix rate of this board (nominal peak 2516.6 TFLOP/s)",
              f"command: {args.command or 'python -m fa_amd.measure.ceiling ' + ' '.join(argv or sys.argv[1:])}"]
-    for shape, rate in gemm().items():
+    for shape, rate in ({} if args.no_gemm else gemm()).items():
         lines.append(f"gemm_fp16 {shape[0]}x{shape[1]}x{shape[2]} (torch.matmul, hipBLASLt): "
                      f"{rate:.1f} TFLOP/s = {rate / clock.PEAK_TFLOPS:.3f} of nominal")
         print(lines[-1], flush=True)
-    for mode, label in ((0, "operands in registers"), (1, "A operand read from LDS"),
-                        (2, "A operand from LDS + the softmax's VALU mix"),
-                        (3, "one LDS operand read per two MFMAs"),
-                        (4, "both operands read from LDS")):
+    modes = [int(m) for m in args.modes.split(",")] if args.modes else [m for m, _ in MODES]
+    for mode in modes:
+        label = MODE_TITLES[mode]
         rate, records = mfma_loop(mode)
         if args.records:
             import numpy as np

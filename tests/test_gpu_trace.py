@@ -66,7 +66,11 @@ def test_ceiling_kernel_runs_and_reports_a_clock():
     lib = ceiling._library()
     # Host-side rejections (nothing is launched): unknown mode, no
     # workgroups, misaligned operands.
-    assert lib.fa_ceiling_mfma(5, 1, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
+    assert lib.fa_ceiling_mfma(7, 1, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
+    assert lib.fa_ceiling_threads(7) == 0 and lib.fa_ceiling_threads(6) == 256
+    assert lib.fa_ceiling_threads(0) == 512
+    assert lib.fa_ceiling_flops(0, 3) == lib.fa_ceiling_flops_per_workgroup(3)
+    assert lib.fa_ceiling_flops(5, 3) * 2 == lib.fa_ceiling_flops_per_workgroup(3)
     assert lib.fa_ceiling_mfma(-1, 1, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
     assert lib.fa_ceiling_mfma(0, 0, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
     assert lib.fa_ceiling_mfma(0, 1, 1, C.c_void_p(24), C.c_void_p(16), None, None) == 1

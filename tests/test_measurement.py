@@ -160,3 +160,30 @@ def test_split_sweep_render():
     assert lines[3] == ("1,12,1,1024,131072: automatic 16 (760 us), fastest 5 (755 us, "
                         "automatic at 1.007x)")
     assert lines[4] == "  1:2195 5:755 16:760"
+
+
+def test_ceiling_library_host_side():
+    """The MFMA ceiling library's launch shapes and FLOP counts, and its
+    host-side rejections (no GPU: nothing is launched)."""
+    import ctypes as C
+
+    from fa_amd import build
+    from fa_amd.measure import ceiling
+
+    if not build.CEILING.library.exists():
+        pytest.skip("libfa_ceiling.so is not built")
+    lib = ceiling._library()
+    per_mfma = 32 * 32 * 16 * 2
+    for mode, _ in ceiling.MODES:
+        threads = 256 if mode in (5, 6) else 512
+        assert lib.fa_ceiling_threads(mode) == threads
+        assert lib.fa_ceiling_flops(mode, 5) == threads // 64 * 5 * 16 * per_mfma
+        assert mode in ceiling.MODE_TITLES
+    assert [m for m, _ in ceiling.MODES] == list(range(7))
+    assert lib.fa_ceiling_threads(7) == 0 and lib.fa_ceiling_threads(-1) == 0
+    assert lib.fa_ceiling_flops_per_workgroup(5) == lib.fa_ceiling_flops(0, 5)
+    for bad in ((7, 1, 1, 16, 16), (-1, 1, 1, 16, 16), (0, 0, 1, 16, 16), (0, 1, 0, 16, 16),
+                (0, 1, 1, 24, 16), (0, 1, 1, 16, 8)):
+        mode, wg, iters, ops, out = bad
+        assert lib.fa_ceiling_mfma(mode, wg, iters, C.c_void_p(ops), C.c_void_p(out), None,
+                                   None) == 1

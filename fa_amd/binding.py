@@ -15,7 +15,9 @@ Mirrors the reference's operator binding
     <status> (<message>)")``;
   * output and workspace tensors are allocated by torch, cached per
     (shapes, device, config), and the same cached output tensor is returned
-    on every call; the workspace grows on demand.
+    on every call; the workspace grows on demand. Calls of one ``Operator``
+    therefore share its output and workspace: forwards that may overlap on
+    different streams need an ``Operator`` each.
 
 Nothing here falls back to another implementation: without the built library
 construction fails.

@@ -155,6 +155,27 @@ class AttentionConfig:
                 raise ValueError("the key-split forward has no capture, trace or sync mode")
 
 
+# Query rows per attention tile.
+TILE_ROWS = 256
+
+
+def query_tiles(batch, heads_q, heads_kv, seq_q):
+    """Attention tiles of one launch, as the library lays them out: unpacked,
+    ``batch * heads_q`` row sequences of ``seq_q`` query rows; packed, when
+    that needs fewer 256-row tiles (grouped-query attention with few query
+    rows), ``batch * heads_kv`` sequences of ``seq_q * group`` rows, the
+    group's query heads position by position. Every row's result is the same
+    either way. (One trace record per tile: ``fa_fwd_trace_count`` / 8.)"""
+    def tiles(seqs, rows):
+        return seqs * -(-rows // TILE_ROWS)
+
+    plain = tiles(batch * heads_q, seq_q)
+    group = heads_q // heads_kv
+    if group <= 1 or seq_q * group >= 2 ** 30:
+        return plain
+    return min(plain, tiles(batch * heads_kv, seq_q * group))
+
+
 def make_problem(q_shape, k_shape, scale, config):
     b, hq, nq, d = q_shape
     _, hkv, nk, _ = k_shape

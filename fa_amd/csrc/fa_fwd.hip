@@ -134,7 +134,7 @@ struct FaArgs {
   int causal, causal_off;
   float c;
   Strides qs, ks, os;
-  // Split mode only (last, so the other modes' argument offsets do not move).
+  // Split mode only (after the others, so their argument offsets do not move).
   float* opart;
   float* lpart;
   int splits;          // key-range parts per tile
@@ -359,7 +359,7 @@ __device__ __forceinline__ void trace_record(const FaArgs& args, int tile, uint6
 // until a block exceeds it by more than TAU, so P <= 2^TAU and the O/l
 // rescale runs only on the rare blocks where some row of the wave needs it.
 // With TAU = 0 the max tracks every increase (FP16 O must not grow).
-template <bool ACC16, int BN, int NS, int MODE>
+template <bool ACC16, int BN, int NS, int MODE, bool PACKED>
 __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, const int split) {
   constexpr bool CAPTURE = MODE == MODE_CAPTURE;
   constexpr bool TRACE = MODE == MODE_TRACE;
@@ -419,14 +419,23 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
   // share a SIMD (round-robin wave placement, read back from HW_ID).
   const int grp = wave_u >> 2;
 
-  // Query tiles may run past Nq (a ragged last tile): its rows past the end
-  // compute on a copy of the last row and store nothing. Without a mask,
-  // consecutive tile indices walk the query tiles of one (batch, head); with
-  // the causal mask, whose tiles differ in work, they walk the heads of one
-  // query tile, the tiles with the most key blocks first, so the short tiles
-  // are taken last.
-  const int tiles_q = (seq_q + BM - 1) / BM;
-  const int nbh = args.tiles / tiles_q;
+  // A tile is 256 consecutive rows of a row sequence. Unpacked, a sequence
+  // is the Nq query rows of one (batch, query head). Packed (PACKED,
+  // grouped-query attention with few query rows), it is the Nq * group rows
+  // of one (batch, KV head) in position-major order: row r is position
+  // r / group of query head kv_head * group + r % group, so the heads that
+  // share K and V fill one tile instead of a tile each. Every row computes
+  // exactly what it computes unpacked (the key loop and its rounding are
+  // per row). A tile may run past the sequence (a ragged last tile): its
+  // rows past the end compute on a copy of the last row and store nothing.
+  // Without a mask, consecutive tile indices walk the tiles of one sequence;
+  // with the causal mask, whose tiles differ in work, they walk the
+  // sequences at one tile position, the tiles with the most key blocks
+  // first, so the short tiles are taken last.
+  constexpr bool packed = PACKED;
+  const int seq_r = packed ? seq_q * group : seq_q;     // rows per sequence
+  const int tiles_q = (seq_r + BM - 1) / BM;
+  const int nbh = args.tiles / tiles_q;                  // sequences
   int bh, qt;
   if (args.causal) {
     const int r = tile / nbh;
@@ -436,15 +445,22 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
     bh = tile / tiles_q;
     qt = tile - bh * tiles_q;
   }
-  const int b = bh / heads_q, h = bh - b * heads_q;
   const int heads_kv = heads_q / group;
-  const size_t kv = (size_t)b * heads_kv + h / group;
-  const _Float16* kp = row_at(k, args.ks, b, h / group, 0);
+  const int b = bh / (packed ? heads_kv : heads_q);
+  const int hs = bh - b * (packed ? heads_kv : heads_q);  // the sequence's head (KV head if packed)
+  const int hk = packed ? hs : hs / group;                // KV head
+  const size_t kv = (size_t)b * heads_kv + hk;
+  const _Float16* kp = row_at(k, args.ks, b, hk, 0);
   const _Float16* vp = vt + kv * (size_t)HD * seq_k;
-  const int row = qt * BM + wave_u * 32 + l32;          // this lane's query row in (b, h)
-  const bool row_ok = row < seq_q;
-  const int rowc = row_ok ? row : seq_q - 1;            // the row it loads
-  const size_t grow = (size_t)bh * seq_q + rowc;        // its index in [B * Hq * Nq] (lse, stats)
+  // Query head and position of row r of the sequence.
+  auto head_of = [&](int r) { return packed ? hk * group + r % group : hs; };
+  auto pos_of = [&](int r) { return packed ? r / group : r; };
+  const int row = qt * BM + wave_u * 32 + l32;          // this lane's row of the sequence
+  const bool row_ok = row < seq_r;
+  const int rowc = row_ok ? row : seq_r - 1;            // the row it loads
+  const size_t rows_all = (size_t)(packed ? nbh * group : nbh) * seq_q;   // B * Hq * Nq
+  // Its index in [B * Hq * Nq] (lse, statistics, split parts).
+  const size_t grow = ((size_t)b * heads_q + head_of(rowc)) * seq_q + pos_of(rowc);
   const int krow = (int)(args.ks.n * 2);                 // K row pitch in bytes
 
   // Last key this lane's row sees (klim) and the smallest such limit over the
@@ -454,9 +470,10 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
   int nblk = seq_k / BN;
   int klim = nk_valid - 1, klim_w = nk_valid - 1;
   if (args.causal) {
-    klim = min(klim, row + args.causal_off);
-    klim_w = min(klim_w, qt * BM + wave_u * 32 + args.causal_off);
-    const int kend = min(qt * BM + BM, seq_q) + args.causal_off;   // keys [0, kend) are seen
+    klim = min(klim, pos_of(row) + args.causal_off);
+    klim_w = min(klim_w, pos_of(qt * BM + wave_u * 32) + args.causal_off);
+    // Keys [0, kend) are seen by the tile's last row.
+    const int kend = pos_of(min(qt * BM + BM, seq_r) - 1) + 1 + args.causal_off;
     nblk = kend <= 0 ? 0 : min(nblk, (kend + BN - 1) / BN);
   }
   // Split mode: this work item streams key blocks [kb0, kb1) of the tile
@@ -471,13 +488,13 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
     klim -= kb0 * BN;
     klim_w -= kb0 * BN;
   }
-  const size_t part = (size_t)split * ((size_t)nbh * seq_q) + grow;   // split mode: partial row
+  const size_t part = (size_t)split * rows_all + grow;   // split mode: partial row
   if (nblk == 0) {
     // No row of this tile sees a key (bottom-right mask, Nq > Nk): O = 0 and
     // lse = -inf. Uniform over the workgroup, before any barrier or load.
     if constexpr (CAPTURE) {
       if (hf == 0 && row_ok) {
-        const size_t rows = (size_t)nbh * seq_q, nb = seq_k / BN;
+        const size_t rows = rows_all, nb = seq_k / BN;
         for (size_t j = 0; j < nb; ++j) {
           args.stats[(0 * nb + j) * rows + grow] = -INFINITY;
           args.stats[(1 * nb + j) * rows + grow] = 0.f;
@@ -505,14 +522,16 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<h4*>(row_at(o, args.os, b, h, rowc) + dt * 32 + 8 * g + 4 * hf) = zero;
+        *reinterpret_cast<h4*>(row_at(o, args.os, b, head_of(rowc), pos_of(rowc)) + dt * 32 +
+                               8 * g + 4 * hf) = zero;
     return;
   }
 
   h8 qf[8];
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk)
-    qf[kk] = *reinterpret_cast<const h8*>(row_at(q, args.qs, b, h, rowc) + kk * 16 + hf * 8);
+    qf[kk] = *reinterpret_cast<const h8*>(row_at(q, args.qs, b, head_of(rowc), pos_of(rowc)) +
+                                          kk * 16 + hf * 8);
 
   // Group-0 wave dw issues DMA instructions q = dw + 4m (m < NIW, q < NI);
   // q < KI is K instruction q, otherwise V^T instruction q - KI. The per-lane
@@ -782,7 +801,7 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
     if constexpr (CAPTURE) {         // capture mode: this block's row statistics
       const float z = half_sum(zsum), lrow = half_sum(lsum);
       if (hf == 0 && row_ok) {
-        const size_t rows = (size_t)nbh * seq_q;   // B * Hq * Nq
+        const size_t rows = rows_all;   // B * Hq * Nq
         const size_t nb = seq_k / BN, j = key0 / BN;
         float* st = args.stats + grow;
         st[(0 * nb + j) * rows] = m == NEG_BIG ? -INFINITY : m * c * LN2;
@@ -893,7 +912,7 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
     // Key blocks past the causal diagonal leave every statistic unchanged.
     const float lrow = half_sum(lsum);
     if (hf == 0 && row_ok) {
-      const size_t rows = (size_t)nbh * seq_q, nb = seq_k / BN;
+      const size_t rows = rows_all, nb = seq_k / BN;
       for (size_t j = nblk; j < nb; ++j) {
         args.stats[(0 * nb + j) * rows + grow] = m == NEG_BIG ? -INFINITY : m * c * LN2;
         args.stats[(1 * nb + j) * rows + grow] = lrow;
@@ -928,7 +947,7 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
     return;
   }
   if (args.lse && hf == 0) args.lse[grow] = (__builtin_amdgcn_logf(l) + m * c) * LN2;
-  _Float16* orow = row_at(o, args.os, b, h, rowc);
+  _Float16* orow = row_at(o, args.os, b, head_of(rowc), pos_of(rowc));
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
@@ -987,7 +1006,7 @@ __device__ __forceinline__ FaArgs load_args(uint64_t addr) {
   return r;
 }
 
-template <bool ACC16, int BN, int NS, int MODE>
+template <bool ACC16, int BN, int NS, int MODE, bool PACKED>
 __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   __shared__ int claimed;
   // Work items: query tiles, or in split mode (tile, part) pairs, the parts
@@ -1011,7 +1030,7 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
     // pressure spills.
     uint64_t addr = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
     asm volatile("" : "+s"(addr));
-    fa_pp_tile<ACC16, BN, NS, MODE>(load_args(addr), tile, split);
+    fa_pp_tile<ACC16, BN, NS, MODE, PACKED>(load_args(addr), tile, split);
     // Every wave has read `claimed` (and finished with the LDS ring) before
     // thread 0 claims the next tile.
     __syncthreads();
@@ -1027,17 +1046,20 @@ constexpr int pp_lds_bytes(int bn, int ns) { return ns * (bn * (HD * 2 + 16) + H
 // attributes kernel time to a backend. Template parameters: BN keys per
 // block, NS slots in the LDS ring, MODE (production, capture, trace, sync or split;
 // each mode is a separate kernel, so the production kernels carry none of
-// the debug code). 8 waves of 64 lanes, two per SIMD.
-template <int BN, int NS, int MODE>
+// the debug code), PACKED (tiles of packed rows: the group's query heads
+// position by position, see fa_pp_tile; also separate kernels, so the
+// unpacked ones carry none of its row arithmetic). 8 waves of 64 lanes, two
+// per SIMD.
+template <int BN, int NS, int MODE, bool PACKED>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 hip_fa_fp32acc_kernel(FaArgs args) {
-  fa_pp_body<false, BN, NS, MODE>(args);
+  fa_pp_body<false, BN, NS, MODE, PACKED>(args);
 }
 
-template <int BN, int NS, int MODE>
+template <int BN, int NS, int MODE, bool PACKED>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 hip_fa_fp16acc_kernel(FaArgs args) {
-  fa_pp_body<true, BN, NS, MODE>(args);
+  fa_pp_body<true, BN, NS, MODE, PACKED>(args);
 }
 
 // ----------------------------------------------------------------------------
@@ -1049,21 +1071,23 @@ struct TileConfig {
   const char* name;
   int keys;        // BN
   int lds;         // dynamic LDS bytes per workgroup
-  attn_fn fn[2][kModes];   // [acc][mode]
+  attn_fn fn[2][2][kModes];   // [packed][acc][mode]
 };
 constexpr int kThreads = 512;     // 8 waves
 constexpr int kRows = 256;        // BM: 8 waves x 32 query rows
 constexpr uint64_t kCounterBytes = 256;
 
+#define FA_MODES(KERNEL, BN, NS, PK)                                                        \
+  {&KERNEL<BN, NS, MODE_RUN, PK>, &KERNEL<BN, NS, MODE_CAPTURE, PK>,                         \
+   &KERNEL<BN, NS, MODE_TRACE, PK>, &KERNEL<BN, NS, MODE_SYNC, PK>,                          \
+   &KERNEL<BN, NS, MODE_SPLIT, PK>}
 #define FA_TILE(NAME, BN, NS)                                                               \
   TileConfig {                                                                              \
     NAME, BN, pp_lds_bytes(BN, NS), {                                                       \
-      {&hip_fa_fp32acc_kernel<BN, NS, MODE_RUN>, &hip_fa_fp32acc_kernel<BN, NS, MODE_CAPTURE>, \
-       &hip_fa_fp32acc_kernel<BN, NS, MODE_TRACE>, &hip_fa_fp32acc_kernel<BN, NS, MODE_SYNC>,  \
-       &hip_fa_fp32acc_kernel<BN, NS, MODE_SPLIT>},                                            \
-      {&hip_fa_fp16acc_kernel<BN, NS, MODE_RUN>, &hip_fa_fp16acc_kernel<BN, NS, MODE_CAPTURE>, \
-       &hip_fa_fp16acc_kernel<BN, NS, MODE_TRACE>, &hip_fa_fp16acc_kernel<BN, NS, MODE_SYNC>,  \
-       &hip_fa_fp16acc_kernel<BN, NS, MODE_SPLIT>}                                             \
+      {FA_MODES(hip_fa_fp32acc_kernel, BN, NS, false),                                      \
+       FA_MODES(hip_fa_fp16acc_kernel, BN, NS, false)},                                     \
+      {FA_MODES(hip_fa_fp32acc_kernel, BN, NS, true),                                       \
+       FA_MODES(hip_fa_fp16acc_kernel, BN, NS, true)}                                       \
     }                                                                                       \
   }
 
@@ -1144,10 +1168,28 @@ uint64_t capture_count(const fa_problem* p, const TileConfig* tile, const KeyLay
   return 4ull * (uint64_t)(lay.nk_pad / tile->keys) * (uint64_t)(p->batch * p->heads_q * p->seq_q);
 }
 
-// Query tiles of one attention launch (one per 256 query rows of a (b, h)).
-uint64_t grid_size(const fa_problem* p) {
-  return (uint64_t)(p->batch * p->heads_q) * (uint64_t)((p->seq_q + kRows - 1) / kRows);
+// Row sequences of one attention launch (the kernel's tile rows, see
+// fa_pp_tile): unpacked, B * Hq sequences of Nq query rows; packed, B * Hkv
+// sequences of Nq * group rows (the group's query heads position by
+// position), taken whenever that needs fewer 256-row tiles: grouped-query
+// attention with fewer than 256 query rows per head, or ragged tails that
+// pack tighter. Both give every row the same result bit for bit.
+struct RowLayout {
+  int64_t seqs;   // sequences
+  int64_t rows;   // rows per sequence
+  int64_t pack;   // query heads per position in a sequence: the group if packed, else 1
+  int64_t tiles() const { return seqs * ((rows + kRows - 1) / kRows); }
+};
+RowLayout row_layout(const fa_problem* p) {
+  const int64_t group = p->heads_q / p->heads_kv;
+  const RowLayout plain{p->batch * p->heads_q, p->seq_q, 1};
+  if (group <= 1 || p->seq_q * group >= ((int64_t)1 << 30)) return plain;
+  const RowLayout packed{p->batch * p->heads_kv, p->seq_q * group, group};
+  return packed.tiles() < plain.tiles() ? packed : plain;
 }
+
+// Query tiles of one attention launch (one per 256 rows of a row sequence).
+uint64_t grid_size(const fa_problem* p) { return (uint64_t)row_layout(p).tiles(); }
 
 // Split mode's partial results, after the tile counter in the workspace:
 // the parts' log-sum-exp (FP32 [splits][R], R = B * Hq * Nq) from a 256-byte
@@ -1169,8 +1211,8 @@ constexpr int kMaxSplits = 1024;
 // Split counts the automatic choice considers: every count up to
 // kAutoSplitMax without a mask (the model is a closed form there), these
 // with a causal mask (the model sums over the tiles).
-constexpr int kAutoSplitMax = 64;
-constexpr int kAutoSplitsCausal[] = {2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64};
+constexpr int kAutoSplitMax = 256;
+constexpr int kAutoSplitsCausal[] = {2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64, 96, 128, 192, 256};
 
 // Modelled duration of a launch whose tiles' key ranges are cut into s
 // parts, in units of one key block's time on one workgroup. A work item
@@ -1180,14 +1222,18 @@ constexpr int kAutoSplitsCausal[] = {2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64};
 // (causal) are bounded by max(total / cus, longest item), which the work
 // queue, handing out the longest tiles first, comes close to. A split launch
 // adds the merge kernel: it reads every part's O and lse and writes O, at
-// kMergeBytesPerSecond.
+// kMergeBytesPerSecond, but no faster than one row's walk over its parts
+// (four part loads in flight, kMergeLatency per four), which is what bounds
+// it when the rows are few (decode shapes).
 constexpr double kItemOverhead = 1.5;
 constexpr double kEmptyItem = 0.1;
 constexpr double kMergeBytesPerSecond = 4.0e12;
+constexpr double kMergeLatency = 0.7e-6;
 double split_cost(const fa_problem* p, const TileConfig* tile, const KeyLayout& lay, int s, int cus) {
   const int bn = tile->keys;
   const int64_t nbt = lay.nk_pad / bn;
-  const int64_t nbh = p->batch * p->heads_q, tiles_q = (p->seq_q + kRows - 1) / kRows;
+  const RowLayout rl = row_layout(p);
+  const int64_t nbh = rl.seqs, tiles_q = (rl.rows + kRows - 1) / kRows;
   const double items = (double)(nbh * tiles_q) * s;
   double t = 0.0;
   if (p->causal == FA_CAUSAL_NONE) {
@@ -1197,7 +1243,8 @@ double split_cost(const fa_problem* p, const TileConfig* tile, const KeyLayout& 
     const int64_t off = p->causal == FA_CAUSAL_BOTTOM_RIGHT ? p->seq_k - p->seq_q : 0;
     double total = 0.0, longest = 0.0;
     for (int64_t r = 0; r < tiles_q; ++r) {
-      const int64_t kend = std::min<int64_t>((r + 1) * kRows, p->seq_q) + off;
+      // Keys [0, kend) are seen by the tile's last row (its position + 1).
+      const int64_t kend = (std::min<int64_t>((r + 1) * kRows, rl.rows) - 1) / rl.pack + 1 + off;
       const int64_t vis = kend <= 0 ? 0 : std::min<int64_t>(nbt, (kend + bn - 1) / bn);
       for (int i = 0; i < s; ++i) {
         const int64_t b0 = i * nbt / s, b1 = (i + 1) * nbt / s;
@@ -1210,10 +1257,11 @@ double split_cost(const fa_problem* p, const TileConfig* tile, const KeyLayout& 
     t = std::max(total / cus, longest);
   }
   if (s > 1) {
-    const double rows = (double)nbh * p->seq_q;
+    const double rows = (double)(p->batch * p->heads_q) * p->seq_q;
     const double bytes = rows * (s * (HD * 4.0 + 4.0) + HD * 2.0 + 4.0);
     const double block_seconds = bn == 128 ? 3.4e-6 : 1.8e-6;
-    t += bytes / kMergeBytesPerSecond / block_seconds;
+    const double merge = std::max(bytes / kMergeBytesPerSecond, ((s + 3) / 4) * kMergeLatency);
+    t += merge / block_seconds;
   }
   return t;
 }
@@ -1276,15 +1324,15 @@ int check_strides(const fa_problem* p, const fa_strides* s, const KeyLayout& lay
 // scratch addresses of fa_fwd_noalloc are the library's only host state;
 // setting either twice (two threads racing on a first call) is harmless.
 constexpr int kMaxDevices = 64;
-std::atomic<uint8_t> g_lds_ready[kMaxDevices][kNumTiles][2][kModes];
+std::atomic<uint8_t> g_lds_ready[kMaxDevices][kNumTiles][2][2][kModes];
 
-int ensure_lds_limit(const TileConfig* tile, int acc, int mode) {
+int ensure_lds_limit(const TileConfig* tile, int packed, int acc, int mode) {
   if (tile->lds <= 65536) return FA_OK;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FA_ERR_LAUNCH;
-  std::atomic<uint8_t>& ready = g_lds_ready[dev][tile - kTiles][acc][mode];
+  std::atomic<uint8_t>& ready = g_lds_ready[dev][tile - kTiles][packed][acc][mode];
   if (ready.load(std::memory_order_acquire)) return FA_OK;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(tile->fn[acc][mode]),
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(tile->fn[packed][acc][mode]),
                           hipFuncAttributeMaxDynamicSharedMemorySize, tile->lds) != hipSuccess)
     return FA_ERR_LAUNCH;
   ready.store(1, std::memory_order_release);
@@ -1366,7 +1414,8 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
                    : ex.trace ? MODE_TRACE
                    : ex.sync  ? MODE_SYNC
                               : MODE_RUN;
-  rc = ensure_lds_limit(tile, acc, mode);
+  const int packed = row_layout(p).pack > 1 ? 1 : 0;
+  rc = ensure_lds_limit(tile, packed, acc, mode);
   if (rc) return rc;
   if (!cus) {
     rc = device_cus(&cus);
@@ -1430,7 +1479,7 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
   // One workgroup per CU (the LDS ring leaves room for no second one), never
   // more workgroups than work items.
   const unsigned grid = (unsigned)std::min<uint64_t>(grid_size(p) * splits, (uint64_t)cus);
-  if (hipLaunchKernel(reinterpret_cast<const void*>(tile->fn[acc][mode]), dim3(grid),
+  if (hipLaunchKernel(reinterpret_cast<const void*>(tile->fn[packed][acc][mode]), dim3(grid),
                       dim3(kThreads), attn_args, tile->lds, st) != hipSuccess)
     return FA_ERR_LAUNCH;
   if (splits > 1) {

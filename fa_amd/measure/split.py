@@ -22,9 +22,13 @@ import os
 import sys
 
 # (B, Hq, Hkv, Nq, Nk): the headline's head layout with short query ranges
-# against long keys, a single query row per head, and c0 (B1 N4096).
+# against long keys, one or a few query rows per head (decode: the group's
+# heads share one packed tile), a batched decode with 8 KV heads of 8 query
+# heads each, and c0 (B1 N4096).
 SHAPES = [
     (1, 12, 1, 1, 131072),
+    (1, 12, 1, 16, 131072),
+    (8, 64, 8, 1, 8192),
     (1, 12, 1, 256, 131072),
     (1, 12, 1, 1024, 131072),
     (1, 12, 1, 4096, 131072),
@@ -33,8 +37,9 @@ SHAPES = [
 ]
 PEAK_TFLOPS = 2516.6
 # Explicit part counts of the sweep (counts above a shape's key blocks are skipped).
-SWEEP_COUNTS = [1, 2, 3, 4, 5, 6, 8, 10, 12, 16, 21, 24, 32, 42, 64]
-SWEEP_SHAPES = SHAPES[1:] + [(1, 12, 1, 8192, 8192), (1, 12, 1, 2048, 32768), (1, 4, 1, 2048, 131072)]
+SWEEP_COUNTS = [1, 2, 3, 4, 5, 6, 8, 10, 12, 16, 21, 24, 32, 42, 64, 96, 128, 192, 256]
+SWEEP_SHAPES = SHAPES + [(1, 12, 1, 8192, 8192), (1, 12, 1, 2048, 32768), (1, 4, 1, 2048, 131072),
+                         (1, 12, 1, 1, 32768)]
 
 
 def parse_shape(text):
@@ -113,9 +118,11 @@ def render(rows, acc, command):
              f"command: {command}",
              f"{'B,Hq,Hkv,Nq,Nk':<22} {'tiles':>5} {'parts':>5} {'one-pass us':>12} {'TFLOP/s':>8} "
              f"{'split us':>10} {'TFLOP/s':>8} {'speedup':>7} {'max|diff|':>10}"]
+    from fa_amd import binding
+
     for r in rows:
-        b, hq, _, nq, _ = r["shape"]
-        tiles = b * hq * -(-nq // 256)
+        b, hq, hkv, nq, _ = r["shape"]
+        tiles = binding.query_tiles(b, hq, hkv, nq)
         lines.append(f"{','.join(map(str, r['shape'])):<22} {tiles:>5} {r['parts']:>5} "
                      f"{r['one_us']:>12.1f} {r['one_tflops']:>8.1f} {r['split_us']:>10.1f} "
                      f"{r['split_tflops']:>8.1f} {r['one_us'] / r['split_us']:>6.2f}x "

@@ -13,6 +13,14 @@
  * j <= i + Nk - Nq (bottom-right); a row that sees no key gets O = 0 and
  * lse = -inf.
  *
+ * Tiles: the attention kernel works on tiles of 256 rows of a row sequence,
+ * the Nq query rows of one (b, h), or -- packed, whenever that needs fewer
+ * tiles (grouped-query attention with few query rows per head, e.g. decode)
+ * -- the Nq * (Hq / Hkv) rows of one (b, KV head) in position-major order
+ * (row r is position r / group of query head hkv * group + r % group). A
+ * row's result is the same bit for bit either way; packing only lets the
+ * heads that share K and V share a tile.
+ *
  * Conventions (mirroring the reference's two-phase operator binding):
  *   - every entry point returns 0 on success and a nonzero FA_ERR_* code
  *     otherwise; fa_strerror() names the code;
@@ -177,10 +185,12 @@ int fa_fwd_capture(const fa_problem* p, const void* q, const void* k, const void
  * fa_fwd_trace_count() words), the counterpart of the reference kernel's
  * per-core trace output, which records each core's id and its start and end
  * system-counter values (K32/panel_kernel.h:222-225,340-342; buffer
- * binding.py:44). Tile w covers the 256 query rows 256r .. 256r+255 of one
- * (b, h): w = (b*Hq + h) * ceil(Nq/256) + r without a mask, and
- * w = (ceil(Nq/256) - 1 - r) * B*Hq + b*Hq + h with a causal mask (longest
- * tiles first). Record of tile w, words 8w .. 8w+7:
+ * binding.py:44). Tile w covers rows 256r .. 256r+255 of row sequence s (see
+ * Tiles above: S sequences of R rows, S = B*Hq and R = Nq unpacked, S =
+ * B*Hkv and R = Nq*Hq/Hkv packed, s = b*Hq + h or b*Hkv + hkv): w = s *
+ * ceil(R/256) + r without a mask, and w = (ceil(R/256) - 1 - r) * S + s with
+ * a causal mask (longest tiles first). fa_fwd_trace_count() / 8 is the
+ * number of tiles. Record of tile w, words 8w .. 8w+7:
  *   0  HW_ID register (bits 0-31) and XCC_ID (bits 32-35) of wave 0 of the
  *      workgroup that ran the tile
  *   1  s_memrealtime when the tile starts (100 MHz reference clock)
@@ -292,9 +302,10 @@ int fa_fwd_split(const fa_problem* p, int32_t splits, const fa_strides* strides,
                  uint64_t workspace_bytes, void* stream);
 /* fa_fwd_split_count: the effective part count for a requested one (0 =
  * automatic) on a GPU with `cus` compute units (0 = the current device's):
- * the automatic choice models the launch's duration per candidate count
- * (work items per CU, per-item overhead, the merge's HBM traffic) and splits
- * only when that beats one pass over the keys by 10 %. */
+ * the automatic choice models the launch's duration per candidate count up
+ * to 256 (work items per CU, per-item overhead, the merge's HBM traffic or,
+ * with few rows, its walk over the parts) and splits only when that beats
+ * one pass over the keys by 10 %. */
 
 /* Static message for a status code. */
 const char* fa_strerror(int status);

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+from fa_amd import binding
 from fa_amd.binding import AttentionConfig, Operator
 
 pytestmark = pytest.mark.gpu
@@ -41,8 +42,11 @@ def test_trace_records_and_identical_output(library_path, acc, nq, nk, causal):
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     rec = traced.last["trace"].cpu().numpy()
-    tiles = -(-nq // 256)
-    assert rec.shape == (b * hq * tiles, 8)
+    # nq = 600 packs the 3 query heads of each KV head into 8 tiles per
+    # (batch, KV head) instead of 3 x 3 per (batch, query head).
+    tiles = binding.query_tiles(b, hq, hkv, nq)
+    assert rec.shape == (tiles, 8)
+    assert tiles < b * hq * -(-nq // 256) or nq != 600
     assert np.array_equal(rec[:, 5], np.arange(rec.shape[0]))
     bn = int(rec[0, 7])
     assert bn in (64, 128) and np.all(rec[:, 7] == bn)

@@ -133,22 +133,48 @@ def test_capture_count_and_rejections(lib):
 
 
 def test_trace_count_and_rejections(lib):
-    # One 8-word record per query tile: B * Hq * ceil(Nq / 256) tiles.
+    # One 8-word record per query tile. Nq = 300 rows of 12 query heads that
+    # share one KV head pack into ceil(3600 / 256) = 15 tiles per batch
+    # instead of 12 x 2 (position-major rows of the whole group).
     prob = problem(batch=2, seq_q=300, seq_k=1000)
     count = C.c_uint64()
     assert lib.fa_fwd_trace_count(C.byref(prob), C.byref(count)) == 0
-    assert count.value == 8 * 2 * 12 * 2
+    assert count.value == 8 * 2 * 15
     assert lib.fa_fwd_trace_count(C.byref(prob), None) == 1
     assert lib.fa_fwd_trace_count(C.byref(problem(dim=64)), C.byref(count)) == 3
     p = C.c_void_p(4096)
     _, size = ws_bytes(lib, prob)
-    need = 8 * 2 * 12 * 2
+    need = 8 * 2 * 15
     assert lib.fa_fwd_trace(C.byref(prob), p, p, p, p, None, need, p, size, None) == 1
     assert lib.fa_fwd_trace(C.byref(prob), p, p, p, p, p, need - 1, p, size, None) == 13
     assert lib.fa_fwd_trace(C.byref(prob), p, p, p, p, C.c_void_p(4104), need, p, size, None) == 5
     assert b"trace" in lib.fa_strerror(13)
     with pytest.raises(ValueError):
         binding.AttentionConfig(trace=True, capture=True)
+
+
+@pytest.mark.parametrize("b,hq,hkv,nq", [
+    (1, 12, 1, 1), (1, 12, 1, 21), (1, 12, 1, 22), (2, 12, 1, 255), (1, 12, 1, 256),
+    (1, 12, 1, 4096), (2, 12, 1, 300), (2, 6, 2, 600), (2, 6, 2, 1000), (1, 8, 2, 40),
+    (3, 4, 4, 7), (1, 1, 1, 1), (1, 64, 8, 3), (1, 32, 1, 100), (2, 2, 1, 129)])
+def test_query_tiles_match_the_library(lib, b, hq, hkv, nq):
+    # The binding's tile rule is the library's: packed only when it needs
+    # fewer tiles (never for a group of 1 or 256-row multiples per head).
+    count = C.c_uint64()
+    assert lib.fa_fwd_trace_count(C.byref(problem(batch=b, heads_q=hq, heads_kv=hkv, seq_q=nq,
+                                                  seq_k=512)), C.byref(count)) == 0
+    assert count.value == 8 * binding.query_tiles(b, hq, hkv, nq)
+    plain = b * hq * -(-nq // 256)
+    assert binding.query_tiles(b, hq, hkv, nq) <= plain
+    if hq == hkv or nq % 256 == 0:
+        assert binding.query_tiles(b, hq, hkv, nq) == plain
+
+
+def test_packed_decode_split_choice(lib):
+    # One query row per head, 12 heads on one KV head: one packed tile, so
+    # the automatic split spreads its 1024 key blocks over many CUs.
+    rc, n = split_count(lib, problem(seq_q=1, seq_k=131072), 0)
+    assert rc == 0 and n >= 32, n
 
 
 def test_sync_mode_rejections(lib):

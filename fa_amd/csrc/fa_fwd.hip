@@ -314,6 +314,89 @@ __global__ void __launch_bounds__(256) fa_merge_kernel(const float* __restrict__
   }
 }
 
+// The merge for few rows with many parts (decode: a dozen rows, a hundred
+// parts or more), where fa_merge_kernel's cost is one row's walk over its
+// parts: a 256-thread workgroup per row (grid-stride over the rows). The
+// workgroup first finds the row's maximum lse; then its 8 groups of 32 lanes
+// each run fa_merge_kernel's per-lane accumulation over parts g, g + 8,
+// g + 16, ..., and the 8 partial sums of O and of the weights are added
+// through LDS, so the walk is 8 times shorter. Same inputs, outputs and
+// special cases as fa_merge_kernel; only the FP32 summation order differs.
+__global__ void __launch_bounds__(256) fa_merge_wide_kernel(const float* __restrict__ opart,
+                                                            const float* __restrict__ lpart,
+                                                            _Float16* __restrict__ o,
+                                                            float* __restrict__ lse, int splits,
+                                                            int64_t rows, int heads_q, int seq_q,
+                                                            Strides os) {
+  constexpr int G = 8;                      // lane groups per workgroup
+  __shared__ float4 part_o[G][HD / 4];
+  __shared__ float part_w[G];
+  __shared__ float part_m[G];
+  const int sub = threadIdx.x & 31, grp = threadIdx.x >> 5;
+  const size_t pstride = (size_t)rows * HD;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    float mx = -INFINITY;
+    for (int s = threadIdx.x; s < splits; s += 32 * G) mx = fmaxf(mx, lpart[s * rows + row]);
+    mx = max32(mx);
+    if (sub == 0) part_m[grp] = mx;
+    __syncthreads();
+    mx = part_m[0];
+#pragma unroll
+    for (int g = 1; g < G; ++g) mx = fmaxf(mx, part_m[g]);
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, wsum = 0.f;
+    if (mx != -INFINITY) {
+      const float* col = opart + (size_t)row * HD + 4 * sub;
+      const int mine = splits > grp ? (splits - grp + G - 1) / G : 0;   // parts grp + G t
+      auto add = [&](float wi, const float4& v) {
+        a0 = __builtin_fmaf(wi, v.x, a0);
+        a1 = __builtin_fmaf(wi, v.y, a1);
+        a2 = __builtin_fmaf(wi, v.z, a2);
+        a3 = __builtin_fmaf(wi, v.w, a3);
+      };
+      for (int t0 = 0; t0 < mine; t0 += 32) {
+        const int t = t0 + sub;
+        const float ls = t < mine ? lpart[(grp + G * t) * rows + row] : -INFINITY;
+        const float w = ls == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((ls - mx) * (float)LOG2E);
+        wsum += w;
+        const int n = min(32, mine - t0);
+        int i = 0;
+        for (; i + 4 <= n; i += 4) {        // four loads in flight before their FMAs
+          float4 v[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            v[j] = *reinterpret_cast<const float4*>(col + (size_t)(grp + G * (t0 + i + j)) * pstride);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) add(__shfl(w, i + j, 32), v[j]);
+        }
+        for (; i < n; ++i)
+          add(__shfl(w, i, 32),
+              *reinterpret_cast<const float4*>(col + (size_t)(grp + G * (t0 + i)) * pstride));
+      }
+      wsum = sum32(wsum);
+    }
+    part_o[grp][sub] = float4{a0, a1, a2, a3};
+    if (sub == 0) part_w[grp] = wsum;
+    __syncthreads();
+    if (threadIdx.x < HD) {
+      const int d = threadIdx.x;
+      float acc = 0.f, wall = 0.f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float4 pv = part_o[g][d >> 2];
+        acc += (d & 3) == 0 ? pv.x : (d & 3) == 1 ? pv.y : (d & 3) == 2 ? pv.z : pv.w;
+        wall += part_w[g];
+      }
+      const float inv = wall > 0.f ? 1.f / wall : 0.f;
+      const int64_t bh = row / seq_q;
+      const int i = (int)(row - bh * seq_q);
+      const int b = (int)(bh / heads_q), h = (int)(bh - (int64_t)b * heads_q);
+      row_at(o, os, b, h, i)[d] = (_Float16)(acc * inv);
+      if (lse && d == 0) lse[row] = wall > 0.f ? mx + __builtin_amdgcn_logf(wall) * LN2 : -INFINITY;
+    }
+    __syncthreads();                        // LDS is reused by the next row
+  }
+}
+
 // Trace mode: thread 0 writes the tile's record (layout at TRACE_WORDS)
 // with the start stamps real0/clk0 and stamps taken now.
 __device__ __forceinline__ void trace_record(const FaArgs& args, int tile, uint64_t real0,
@@ -1229,6 +1312,11 @@ constexpr double kItemOverhead = 1.5;
 constexpr double kEmptyItem = 0.1;
 constexpr double kMergeBytesPerSecond = 4.0e12;
 constexpr double kMergeLatency = 0.7e-6;
+// fa_merge_wide_kernel takes over from fa_merge_kernel for at most this many
+// rows with at least kMergeWideParts parts (one workgroup per row).
+constexpr int64_t kMergeWideRows = 4096;
+constexpr int kMergeWideParts = 32;
+bool merge_wide(int64_t rows, int splits) { return rows <= kMergeWideRows && splits >= kMergeWideParts; }
 double split_cost(const fa_problem* p, const TileConfig* tile, const KeyLayout& lay, int s, int cus) {
   const int bn = tile->keys;
   const int64_t nbt = lay.nk_pad / bn;
@@ -1260,7 +1348,10 @@ double split_cost(const fa_problem* p, const TileConfig* tile, const KeyLayout& 
     const double rows = (double)(p->batch * p->heads_q) * p->seq_q;
     const double bytes = rows * (s * (HD * 4.0 + 4.0) + HD * 2.0 + 4.0);
     const double block_seconds = bn == 128 ? 3.4e-6 : 1.8e-6;
-    const double merge = std::max(bytes / kMergeBytesPerSecond, ((s + 3) / 4) * kMergeLatency);
+    // A row's walk: four part loads in flight per lane, over all its parts
+    // (fa_merge_kernel) or over an eighth of them (fa_merge_wide_kernel).
+    const int walk = merge_wide((int64_t)rows, s) ? (s + 7) / 8 : s;
+    const double merge = std::max(bytes / kMergeBytesPerSecond, ((walk + 3) / 4) * kMergeLatency);
     t += merge / block_seconds;
   }
   return t;
@@ -1491,9 +1582,12 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
     int64_t rows = p->batch * p->heads_q * p->seq_q;
     int heads_q = (int)p->heads_q, seq_q = (int)p->seq_q;
     void* merge_args[] = {&opart, &lpart, &out, &lse, &nsplit, &rows, &heads_q, &seq_q, &os};
-    const unsigned blocks = (unsigned)std::min<int64_t>((rows + 7) / 8, (int64_t)1 << 20);
-    if (hipLaunchKernel(reinterpret_cast<const void*>(&fa_merge_kernel), dim3(blocks), dim3(256),
-                        merge_args, 0, st) != hipSuccess)
+    const bool wide = merge_wide(rows, splits);
+    const unsigned blocks =
+        (unsigned)std::min<int64_t>(wide ? rows : (rows + 7) / 8, (int64_t)1 << 20);
+    const void* merge_fn = wide ? reinterpret_cast<const void*>(&fa_merge_wide_kernel)
+                                : reinterpret_cast<const void*>(&fa_merge_kernel);
+    if (hipLaunchKernel(merge_fn, dim3(blocks), dim3(256), merge_args, 0, st) != hipSuccess)
       return FA_ERR_LAUNCH;
   }
   return FA_OK;

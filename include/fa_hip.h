@@ -304,8 +304,9 @@ int fa_fwd_split(const fa_problem* p, int32_t splits, const fa_strides* strides,
  * automatic) on a GPU with `cus` compute units (0 = the current device's):
  * the automatic choice models the launch's duration per candidate count up
  * to 256 (work items per CU, per-item overhead, the merge's HBM traffic or,
- * with few rows, its walk over the parts) and splits only when that beats
- * one pass over the keys by 10 %. */
+ * with few rows, its walk over the parts; for at most 4096 rows and 32 parts
+ * or more the merge gives each row a workgroup) and splits only when that
+ * beats one pass over the keys by 10 %. */
 
 /* Static message for a status code. */
 const char* fa_strerror(int status);

@@ -7,7 +7,7 @@
 // one (batch, head), 8 waves x 32 rows. The attention kernel is persistent:
 // one workgroup per CU takes tiles from a counter until none are left. For a
 // tile it streams the whole key range in blocks of BN keys; each K block and
-// V^T block is staged once in LDS (a ring of slots) and read by every wave,
+// V block is staged once in LDS (a ring of slots) and read by every wave,
 // and every wave keeps its Q fragments, O accumulators and softmax
 // statistics in registers for the whole key loop. Ragged query and key tails
 // are masked, the per-row log-sum-exp is written on request, and an optional
@@ -21,14 +21,22 @@
 //   S^T = K Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS, B = Q^T
 //                 from registers. Lane l holds query row l%32 and 16 keys
 //                 per 32x32 tile.
-//   O^T += V^T P^T  A = V^T rows from LDS, B = P^T straight from the S^T
+//   O^T += V^T P^T  A = V^T from LDS, B = P^T straight from the S^T
 //                 registers (converted to FP16). Lane l keeps query row l%32
 //                 for all its O registers, so rescaling by alpha is per lane.
 // The 32x32 output layout gives a lane keys {8g+4h .. 8g+4h+3} (g = 0..3,
 // h = lane/32); the PV step over keys 16s..16s+15 therefore wants, in its k
-// slots 8h..8h+7, keys {16s+4h..+3, 16s+8+4h..+3}. The prep kernel writes
-// V^T with exactly that key order inside every 16-key group, so each A
-// fragment is one 16-byte LDS read.
+// slots 8h..8h+7 of dim d = lane%32, keys {16s+4h..+3, 16s+8+4h..+3}: two
+// runs of 4 consecutive keys down one column of V. Two ways to feed it:
+//   * V^T tiles: a prep kernel writes V^T with exactly that key order inside
+//     every 16-key group, so each A fragment is one 16-byte LDS read;
+//   * the natural-V tile: V is staged in LDS as it lies in memory ([key][dim]
+//     rows, like K), and each A fragment is two transposing LDS reads
+//     (ds_read_b64_tr_b16, gfx950), each giving every lane 4 keys of its dim.
+// The second needs no pass over V before the attention kernel and no V^T
+// workspace, at the price of twice the V operand read instructions (about
+// 1.5 % of the key loop); the automatic tile choice takes it where that
+// pass is the larger cost (few query rows per KV head).
 //
 // Online softmax in base 2 with the scale folded in (c = scale*log2(e)):
 //   m' = max(m, rowmax(S)),  alpha = 2^((m - m') c),  P = 2^(S c - m' c),
@@ -60,7 +68,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int HD = 128;               // head dimension
-constexpr int VT_GROUP = 64;          // keys per prep-kernel workgroup
+constexpr int PAD_GROUP = 64;         // keys per prep-kernel workgroup
 constexpr float NEG_BIG = -1.0e30f;   // finite "minus infinity" for the running max
 // Added to the score of a masked key: far below any real score
 // (|scale * q.k| <= 128 * 65504^2 ~ 5.5e11) and below NEG_BIG, so the key
@@ -98,7 +106,10 @@ constexpr uint32_t NAN16X2 = 0x7e007e00u;
 // The shader clock the tile ran at is (w4 - w3) / (w2 - w1) * 100 MHz.
 constexpr int TRACE_WORDS = 8;
 
-// Kernel arguments. seq_k is the key length of the K and V^T buffers the
+// Kernel arguments. v is the V buffer the kernel reads: the prep kernel's
+// V^T (contiguous, 128 rows of seq_k keys per KV head) or, for the tile that
+// reads V in its natural layout, the caller's v or its padded copy. seq_k is
+// the key length of the K and V buffers the
 // kernel reads (a multiple of its key block); keys at or past nk_valid are
 // zero padding and masked out of the softmax. lse (FP32 [B, Hq, Nq],
 // natural-log log-sum-exp of the scaled scores) may be null. stats, when not
@@ -110,9 +121,9 @@ constexpr int TRACE_WORDS = 8;
 // one record of TRACE_WORDS 64-bit words per query tile (see trace_record). c is the softmax scale times
 // log2(e). With causal set, query row i sees keys j <= i + causal_off only
 // (causal_off = 0 aligns the mask top-left, Nk - Nq bottom-right); a row that
-// sees no key gets O = 0 and lse = -inf. qs, ks and os are the element
-// strides of q, of the K buffer read (the caller's k, or its padded
-// contiguous copy) and of o. In split mode (splits >= 2) the kernel writes,
+// sees no key gets O = 0 and lse = -inf. qs, ks, vs and os are the element
+// strides of q, of the K and natural-layout V buffers read (the caller's k
+// and v, or their padded contiguous copies) and of o. In split mode (splits >= 2) the kernel writes,
 // instead of o and lse, each part's O normalised by its own row sum into
 // opart (FP32 [splits][B * Hq * Nq][128]) and the part's natural-log
 // log-sum-exp into lpart (FP32 [splits][B * Hq * Nq]; -inf for a part in
@@ -123,7 +134,7 @@ struct Strides {
 struct FaArgs {
   const _Float16* q;
   const _Float16* k;
-  const _Float16* vt;
+  const _Float16* v;
   _Float16* o;
   float* lse;
   float* stats;
@@ -138,6 +149,7 @@ struct FaArgs {
   float* opart;
   float* lpart;
   int splits;          // key-range parts per tile
+  Strides vs;
 };
 
 // Row n of head h of batch b of a strided [B, H, N, 128] tensor.
@@ -171,25 +183,26 @@ __device__ __forceinline__ int vt_key_of_slot(int slot) {
   return (e < 4) ? (4 * h + e) : (8 + 4 * h + (e - 4));
 }
 
-// vt[kv][d][key0 + slot] = v[kv][key0 + key(slot)][d], one 64-key group per
-// workgroup; keys at or past nk_valid become zeros. With kpad non-null the
-// group's K rows are also copied to kpad[kv][key0 + r] (zero rows past
-// nk_valid), the padded K a masked key tail reads. Grid (nk_pad / 64, B * Hkv),
-// 256 threads; v and k hold nk_valid keys per head with strides vs and ks,
-// vt and kpad are contiguous with nk_pad keys per head. It also resets the
-// attention kernel's tile counter.
+// Prep for the tiles that read V transposed: vt[kv][d][key0 + slot] =
+// v[kv][key0 + key(slot)][d], one 64-key group per workgroup; keys at or past
+// nk_valid become zeros. With kpad non-null the group's K rows are also
+// copied to kpad[kv][key0 + r] (zero rows past nk_valid), the padded K a
+// masked key tail reads. Grid (nk_pad / 64, B * Hkv), 256 threads; v and k
+// hold nk_valid keys per head with strides vs and ks, vt and kpad are
+// contiguous with nk_pad keys per head. It also resets the attention
+// kernel's tile counter.
 __global__ void __launch_bounds__(256) fa_prep_kernel(const _Float16* __restrict__ k,
                                                       const _Float16* __restrict__ v,
                                                       _Float16* __restrict__ vt,
                                                       _Float16* __restrict__ kpad, int nk_valid,
                                                       int nk_pad, int heads_kv, Strides ks,
                                                       Strides vs, int* __restrict__ next_tile) {
-  __shared__ _Float16 tile[VT_GROUP][HD + 8];
+  __shared__ _Float16 tile[PAD_GROUP][HD + 8];
   const int tid = threadIdx.x;
   if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) *next_tile = 0;   // the attention kernel's work queue
   const size_t kv = blockIdx.y;
   const int b = (int)(kv / heads_kv), hk = (int)(kv % heads_kv);
-  const int key0 = blockIdx.x * VT_GROUP;
+  const int key0 = blockIdx.x * PAD_GROUP;
   _Float16* kdst = kpad ? kpad + (kv * nk_pad + key0) * HD : nullptr;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -217,6 +230,75 @@ __global__ void __launch_bounds__(256) fa_prep_kernel(const _Float16* __restrict
     }
     *reinterpret_cast<h8*>(dst + (size_t)d * nk_pad + ch * 8) = val;
   }
+}
+
+// Prep for the tile that reads V in its natural layout: resets the attention
+// kernel's tile counter and, for a ragged key tail (kpad non-null), writes
+// zero-padded copies of K and V: kpad[kv][key] and vpad[kv][key] hold the
+// caller's rows for keys below nk_valid and zeros up to nk_pad, one 64-key
+// group per workgroup (grid (nk_pad / 64, B * Hkv), 256 threads; k and v hold
+// nk_valid keys per head with strides ks and vs, the copies are contiguous).
+// Without a tail the attention kernel reads the caller's k and v themselves,
+// and this kernel runs as one workgroup.
+__global__ void __launch_bounds__(256) fa_pad_kernel(const _Float16* __restrict__ k,
+                                                     const _Float16* __restrict__ v,
+                                                     _Float16* __restrict__ kpad,
+                                                     _Float16* __restrict__ vpad, int nk_valid,
+                                                     int nk_pad, int heads_kv, Strides ks,
+                                                     Strides vs, int* __restrict__ next_tile) {
+  const int tid = threadIdx.x;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) *next_tile = 0;   // the attention kernel's work queue
+  if (!kpad) return;
+  const size_t kv = blockIdx.y;
+  const int b = (int)(kv / heads_kv), hk = (int)(kv % heads_kv);
+  const int key0 = blockIdx.x * PAD_GROUP;
+  _Float16* kdst = kpad + (kv * nk_pad + key0) * HD;
+  _Float16* vdst = vpad + (kv * nk_pad + key0) * HD;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = tid + 256 * j;
+    const int r = i >> 4, ch = i & 15;
+    const bool valid = key0 + r < nk_valid;
+    *reinterpret_cast<u32x4*>(kdst + (size_t)r * HD + ch * 8) =
+        valid ? *reinterpret_cast<const u32x4*>(row_at(k, ks, b, hk, key0 + r) + ch * 8) : zero;
+    *reinterpret_cast<u32x4*>(vdst + (size_t)r * HD + ch * 8) =
+        valid ? *reinterpret_cast<const u32x4*>(row_at(v, vs, b, hk, key0 + r) + ch * 8) : zero;
+  }
+}
+
+// The LDS word a transposing read returns: ds_read_b64_tr_b16 with lane j
+// pointing at 4 consecutive FP16 values gives, in each group of 16 lanes,
+// lane l the values at offset l % 4 of the 4 lanes 4e + (l % 16) / 4 of its
+// group (e = 0..3): the 4 x 16 block those lanes address, read by column.
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 tr_h4;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ h4 lds_read_tr(const char* p) {
+  const tr_h4 r = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+      (__attribute__((address_space(3))) tr_h4*)(p));
+  return __builtin_bit_cast(h4, r);
+}
+
+// Raw-buffer descriptor (gfx9 layout: base address, stride 0, range in
+// bytes, 32-bit data format) for loads from `base`; the hardware returns
+// zeros for any lane whose offset lies at or past `bytes`.
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, int bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), bytes, 0x00020000};
+}
+
+// One direct-to-LDS load: 64 lanes x 16 bytes from the buffer `rsrc` at byte
+// offset voff (per lane) + soff (wave-uniform) into the 1 KiB of LDS at byte
+// address lds_addr (wave-uniform; M0 holds it for the load). Written as
+// inline assembly so that the compiler does not track these loads: it
+// orders a transposing LDS read (ds_read_b64_tr_b16) after every load into
+// LDS still in flight (vmcnt(0)), which would stall each MFMA step on the
+// loads meant for later blocks. The attention body orders its loads and
+// operand reads itself (explicit vmcnt waits before the barriers that
+// publish a block), and nothing else in these kernels uses M0.
+__device__ __forceinline__ void dma_to_lds(i32x4 rsrc, uint32_t lds_addr, int voff, int soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff) : "memory");
 }
 
 // Workgroup barrier that also drains this wave's outstanding LDS operations,
@@ -427,7 +509,7 @@ __device__ __forceinline__ void trace_record(const FaArgs& args, int tile, uint6
 // on every SIMD one wave keeps the matrix pipe busy while the other does its
 // softmax (the FA3 ping-pong schedule, here across the two waves of a SIMD).
 //
-// LDS holds a ring of NS K blocks and NS V^T blocks (NS >= 2). Phase pair t
+// LDS holds a ring of NS K blocks and NS V blocks (NS >= 2). Phase pair t
 // (phases 2t, 2t+1) reads K(t) and V(t-1). In phase 2t the direct-to-LDS
 // loads (buffer_load_dwordx4 ... lds, 1 KiB per wave instruction) of
 // K(t+NS-1) and V(t+NS-2) go out into the ring slots pair t-1 finished with:
@@ -442,7 +524,19 @@ __device__ __forceinline__ void trace_record(const FaArgs& args, int tile, uint6
 // until a block exceeds it by more than TAU, so P <= 2^TAU and the O/l
 // rescale runs only on the rare blocks where some row of the wave needs it.
 // With TAU = 0 the max tracks every increase (FP16 O must not grow).
-template <bool ACC16, int BN, int NS, int MODE, bool PACKED>
+// LDS ring slots of the ping-pong body, in 16-byte chunks. A K block is BN
+// rows of 128 dims as they lie in memory, 17 chunks per row (16 + 1 pad). A V
+// block is either V^T, the key-permuted transposed copy the prep kernel
+// writes (128 dim rows of BN keys, BN / 8 + 1 chunks per row), or, in the
+// tile that reads V in its natural layout (VNAT), BN key rows of 128 dims,
+// 16 chunks per row with no pad: row r holds its chunk c at position
+// c ^ 4 (r % 4), which spreads the 4 rows a transposing read takes its
+// columns from over the 4 quarters of the banks.
+constexpr int K_CHUNKS = 17;
+constexpr int k_block_bytes(int bn) { return bn * K_CHUNKS * 16; }
+constexpr int v_block_bytes(int bn, bool vnat) { return vnat ? bn * HD * 2 : HD * (bn / 8 + 1) * 16; }
+
+template <bool ACC16, int BN, int NS, int MODE, bool PACKED, bool VNAT>
 __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, const int split) {
   constexpr bool CAPTURE = MODE == MODE_CAPTURE;
   constexpr bool TRACE = MODE == MODE_TRACE;
@@ -455,7 +549,7 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
   }
   const _Float16* __restrict__ q = args.q;
   const _Float16* __restrict__ k = args.k;
-  const _Float16* __restrict__ vt = args.vt;
+  const _Float16* __restrict__ v = args.v;
   _Float16* __restrict__ o = args.o;
   const int heads_q = args.heads_q, group = args.group, seq_q = args.seq_q, seq_k = args.seq_k;
   const int nk_valid = args.nk_valid;
@@ -467,18 +561,22 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
   constexpr int NQK = 8 * KT;            // QK MFMAs per block
   constexpr int NPV = 4 * KS;            // PV MFMAs per block
   static_assert(NQK == NPV, "QK and PV MFMA counts pair up");
-  // Padded LDS rows: one extra 16-byte chunk per row makes the 32 rows a
-  // wave reads at one chunk column hit distinct bank groups, and keeps every
-  // operand address "lane base + immediate".
-  constexpr int KROW = HD * 2 + 16;      // bytes per K row
-  constexpr int VROW = BN * 2 + 16;      // bytes per V^T row
-  constexpr int KBYTES = BN * KROW;
-  constexpr int VBYTES = HD * VROW;
-  constexpr int VCPR = BN / 8;           // data chunks per V^T row
+  // Padded K and V^T rows keep every operand address "lane base + immediate"
+  // and spread a read over the banks: the extra chunk per row makes the 32
+  // rows a wave reads at one chunk column (ds_read_b128) hit distinct bank
+  // groups. Natural V rows are swizzled instead (v_block_bytes): each
+  // half-wave of a transposing read addresses 4 rows x 64 bytes, which the
+  // swizzle puts in the 4 distinct quarters of the 64 banks.
+  constexpr int KROW = K_CHUNKS * 16;                  // bytes per K row
+  constexpr int VCH = VNAT ? HD / 8 : BN / 8 + 1;      // chunks per V (or V^T) row
+  constexpr int VDATA = VNAT ? HD / 8 : BN / 8;        // of which data chunks
+  constexpr int VROW = VCH * 16;                       // bytes per V (or V^T) row
+  constexpr int KBYTES = k_block_bytes(BN);
+  constexpr int VBYTES = v_block_bytes(BN, VNAT);
   // Direct-to-LDS loads fill 1 KiB of consecutive LDS per wave instruction,
   // pad chunks included (they receive a harmless copy of chunk 0 of the row).
-  constexpr int KI = BN * 17 / 64;       // DMA instructions per K block
-  constexpr int VI = HD * (VCPR + 1) / 64;   // DMA instructions per V^T block
+  constexpr int KI = KBYTES / 1024;      // DMA instructions per K block
+  constexpr int VI = VBYTES / 1024;      // DMA instructions per V block
   constexpr int NI = KI + VI;            // per phase pair, spread over group 0
   constexpr int NIW = (NI + 3) / 4;      // most instructions one group-0 wave issues
   static_assert(KBYTES == KI * 1024 && VBYTES == VI * 1024, "blocks are whole DMA instructions");
@@ -487,7 +585,7 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
 
   extern __shared__ __attribute__((aligned(16))) char lds[];
   char* kbase = lds;                     // NS K blocks
-  char* vbase = lds + NS * KBYTES;       // NS V^T blocks
+  char* vbase = lds + NS * KBYTES;       // NS V blocks
 
   // The thread index passes through an opaque move, so nothing derived from
   // it is hoisted out of the work-queue loop around this function: values a
@@ -534,7 +632,8 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
   const int hk = packed ? hs : hs / group;                // KV head
   const size_t kv = (size_t)b * heads_kv + hk;
   const _Float16* kp = row_at(k, args.ks, b, hk, 0);
-  const _Float16* vp = vt + kv * (size_t)HD * seq_k;
+  // This KV head's V rows (natural layout) or V^T rows (128 rows of seq_k keys).
+  const _Float16* vp = VNAT ? row_at(v, args.vs, b, hk, 0) : v + kv * (size_t)HD * seq_k;
   // Query head and position of row r of the sequence.
   auto head_of = [&](int r) { return packed ? hk * group + r % group : hs; };
   auto pos_of = [&](int r) { return packed ? r / group : r; };
@@ -545,6 +644,7 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
   // Its index in [B * Hq * Nq] (lse, statistics, split parts).
   const size_t grow = ((size_t)b * heads_q + head_of(rowc)) * seq_q + pos_of(rowc);
   const int krow = (int)(args.ks.n * 2);                 // K row pitch in bytes
+  const int vrow = VNAT ? (int)(args.vs.n * 2) : seq_k * 2;   // V (or V^T) row pitch in bytes
 
   // Last key this lane's row sees (klim) and the smallest such limit over the
   // wave (klim_w, wave-uniform: the wave's first row); blocks reaching past
@@ -617,47 +717,47 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
                                           kk * 16 + hf * 8);
 
   // Group-0 wave dw issues DMA instructions q = dw + 4m (m < NIW, q < NI);
-  // q < KI is K instruction q, otherwise V^T instruction q - KI. The per-lane
-  // source offset inside a block is fixed, so it is computed once.
+  // q < KI is K instruction q, otherwise V instruction q - KI. The per-lane
+  // source offset inside a block is fixed, so it is computed once. Natural V
+  // instruction q' fills rows 4q' .. 4q' + 3 with no pad chunks, so all of
+  // them share one per-lane offset (vdma: row lane / 16 of the four, the
+  // chunk its swizzled position holds) and differ by 4q' rows, a scalar.
   const int dw = wave_u & 3;
-  int dma_off[NIW];
+  constexpr int NKW = (KI + 3) / 4;      // most K instructions one wave issues
+  constexpr int NOFF = VNAT ? NKW : NIW;  // per-lane offsets kept
+  const int vdma = (lane >> 4) * vrow + ((lane & 15) ^ (4 * ((lane >> 4) & 3))) * 16;
+  int dma_off[NOFF];
 #pragma unroll
-  for (int m = 0; m < NIW; ++m) {
+  for (int m = 0; m < NOFF; ++m) {
     const int q = dw + 4 * m;
     if (q < KI) {
       const int i = q * 64 + lane, r = i / 17, ch = i % 17;
       dma_off[m] = r * krow + (ch < 16 ? ch : 0) * 16;
+    } else if constexpr (VNAT) {
+      dma_off[m] = vdma;
     } else {
-      const int i = (q - KI) * 64 + lane, d = i / (VCPR + 1), ch = i % (VCPR + 1);
-      dma_off[m] = d * seq_k * 2 + (ch < VCPR ? ch : 0) * 16;
+      const int i = (q - KI) * 64 + lane, r = i / VCH, ch = i % VCH;
+      dma_off[m] = r * vrow + (ch < VDATA ? ch : 0) * 16;
     }
   }
   // The loads are buffer loads through one descriptor per operand (base =
-  // this KV head's K or V^T, range = the bytes its seq_k rows span, so the
+  // this KV head's K or V, range = the bytes its seq_k rows span, so the
   // hardware bounds-checks every lane): the per-lane offset is dma_off, the
-  // block offset a wave-uniform scalar. Buffer (MUBUF) loads rather than
-  // global_load_lds: the compiler counts a FLAT-encoded load into LDS as a
-  // possible LDS access of unknown order and waits for every outstanding LDS
-  // read (lgkmcnt(0)) after each one, which drained the operand prefetch
-  // of the MFMA step; buffer loads are counted on vmcnt only.
-  constexpr int RSRC_WORD3 = 0x00020000;   // gfx9 raw-buffer descriptor: 32-bit data format
-  const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(kp + (size_t)kb0 * BN * args.ks.n), (short)0, (seq_k - kb0 * BN - 1) * krow + HD * 2,
-      RSRC_WORD3);
-  const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(vp + kb0 * BN), (short)0, seq_k * (HD * 2) - kb0 * (BN * 2), RSRC_WORD3);
-  // DMA instruction m of this wave for K block kb -> ring slot ks and V^T
-  // block vb -> slot vs. Branch free: the K/V^T choice is a select on
+  // block offset a wave-uniform scalar (see dma_to_lds).
+  const i32x4 krsrc = buffer_rsrc(kp + (size_t)kb0 * BN * args.ks.n, (seq_k - kb0 * BN - 1) * krow + HD * 2);
+  const i32x4 vrsrc = VNAT ? buffer_rsrc(vp + (size_t)kb0 * BN * args.vs.n, (seq_k - kb0 * BN - 1) * vrow + HD * 2)
+                           : buffer_rsrc(vp + kb0 * BN, seq_k * (HD * 2) - kb0 * (BN * 2));
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+  // DMA instruction m of this wave for K block kb -> ring slot ks and V
+  // block vb -> slot vs. Branch free: the K/V choice is a select on
   // wave-uniform values; only a wave's last instruction can be absent.
   auto dma_one = [&](int m, int kb, int ks, int vb, int vs) {
     const int q = dw + 4 * m;
     if (m == NIW - 1 && NI % 4 != 0 && q >= NI) return;
     const bool isk = q < KI;
-    char* dst = isk ? kbase + ks * KBYTES + q * 1024 : vbase + vs * VBYTES + (q - KI) * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(isk ? krsrc : vrsrc,
-                                             (__attribute__((address_space(3))) void*)dst, 16,
-                                             dma_off[m], isk ? kb * (BN * krow) : vb * (BN * 2),
-                                             0, 0);
+    const int dst = isk ? ks * KBYTES + q * 1024 : NS * KBYTES + vs * VBYTES + (q - KI) * 1024;
+    const int soff = isk ? kb * (BN * krow) : VNAT ? (vb * BN + 4 * (q - KI)) * vrow : vb * (BN * 2);
+    dma_to_lds(isk ? krsrc : vrsrc, lds0 + dst, m < NOFF ? dma_off[m] : vdma, soff);
   };
   auto issue = [&](int kb, int ks, int vb, int vs) {
 #pragma unroll
@@ -685,11 +785,17 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
       case 15: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
       case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
       case 17: asm volatile("s_waitcnt vmcnt(17)" ::: "memory"); break;
-      default: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+      case 18: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+      case 19: asm volatile("s_waitcnt vmcnt(19)" ::: "memory"); break;
+      case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
+      case 21: asm volatile("s_waitcnt vmcnt(21)" ::: "memory"); break;
+      case 22: asm volatile("s_waitcnt vmcnt(22)" ::: "memory"); break;
+      case 23: asm volatile("s_waitcnt vmcnt(23)" ::: "memory"); break;
+      default: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  static_assert((NS - 2) * NIW <= 18 && NS >= 2, "wait_dma covers at most 18 loads");
+  static_assert((NS - 2) * NIW <= 24 && NS >= 2, "wait_dma covers at most 24 loads");
   // MFMA index after which DMA instruction m is issued inside an MFMA step.
   constexpr int DSTEP = (2 * NQK - 8) / NIW > 0 ? (2 * NQK - 8) / NIW : 1;
   static_assert(1 + DSTEP * (NIW - 1) < 2 * NQK, "every DMA instruction finds an MFMA slot");
@@ -723,10 +829,24 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
   for (int i = 0; i < KS; ++i) p[i] = h8{};
   const h2 ones = {(_Float16)1.f, (_Float16)1.f};
 
-  // Per-lane operand offsets: QK op (t, kk) reads K row 32t + l32, chunk
-  // 2kk + hf; PV op (dt, ks) reads V^T row 32dt + l32, chunk 2ks + hf.
+  // Per-lane operand offsets. QK op (t, kk) reads K row 32t + l32, chunk
+  // 2kk + hf. PV op (dt, ks) needs, for dim 32dt + l32, the keys 16ks + 4hf
+  // + {0..3} and + {8..11}: from V^T, row 32dt + l32, chunk 2ks + hf (one
+  // 16-byte read); from natural V, two transposing reads, in which lane j =
+  // 16g + 4e + i (g = j / 16) points at V row 16ks + 4(g / 2) + e (+ 8 for the
+  // second), dims 32dt + 16(g % 2) + 4i .. + 3: chunk 4dt + 2(g % 2) + i / 2,
+  // stored at position 4(dt ^ e) + 2(g % 2) + i / 2 of a row with r % 4 = e.
+  // That position depends on dt and on the lane, so natural V keeps one
+  // base per dt.
   const int k_lane = l32 * KROW + hf * 16;
   const int v_lane = l32 * VROW + hf * 16;
+  int v_nat[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    const int e = (lane & 15) >> 2;
+    v_nat[dt] = (4 * hf + e) * VROW + (4 * (dt ^ e) + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)) * 16 +
+                (lane & 1) * 8;
+  }
 
   // MFMA step for block j: S^T(j) = K(j) Q^T and O^T += V^T(j-1) P^T(j-1),
   // QK and PV MFMAs interleaved, operands prefetched PF MFMAs ahead.
@@ -741,7 +861,13 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
       return *reinterpret_cast<const h8*>(kb + k_lane + t * 32 * KROW + kk * 32);
     }
     const int dt = n % 4, ks = n / 4;
-    return *reinterpret_cast<const h8*>(vb + v_lane + dt * 32 * VROW + ks * 32);
+    if constexpr (VNAT) {
+      const char* at = vb + v_nat[dt] + ks * 16 * VROW;
+      return __builtin_shufflevector(lds_read_tr(at), lds_read_tr(at + 8 * VROW), 0, 1, 2, 3, 4, 5, 6,
+                                     7);
+    } else {
+      return *reinterpret_cast<const h8*>(vb + v_lane + dt * 32 * VROW + ks * 32);
+    }
   };
   // The step's first PF operands. A group-1 wave reads them at the end of
   // the VALU step before its MFMA step (its blocks were published one phase
@@ -776,13 +902,13 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
   };
 
   if constexpr (SYNC) {
-    // Poison the whole ring (every K and V^T slot, row pads included), so an
+    // Poison the whole ring (every K and V slot, row pads included), so an
     // operand read of LDS that no load of this tile has written is a NaN.
     for (int i = tid; i < NS * (KBYTES + VBYTES) / 16; i += NT)
       reinterpret_cast<u32x4*>(lds)[i] = u32x4{NAN16X2, NAN16X2, NAN16X2, NAN16X2};
     lds_barrier();
   }
-  // V^T slot NS-1 (read as "V(-1)" by the first MFMA step) starts as zeros:
+  // V slot NS-1 (read as "V(-1)" by the first MFMA step) starts as zeros:
   // the first step multiplies it by P = 0.
   for (int i = tid; i < VBYTES / 16; i += NT)
     reinterpret_cast<u32x4*>(vbase + (NS - 1) * VBYTES)[i] = u32x4{0u, 0u, 0u, 0u};
@@ -791,14 +917,21 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
   // Prologue (group 0): K(0..NS-2) -> slots 0..NS-2 and V(0..NS-3) -> slots
   // 0..NS-3, everything pairs before pair 0 would have loaded. Block indices
   // past the end are clamped, so every pair issues the same loads and the
-  // fixed wait counts stay exact. (issue() always loads one K and one V^T
-  // block; the prologue's extra V^T loads target slots that are rewritten
+  // fixed wait counts stay exact. (issue() always loads one K and one V
+  // block; the prologue's extra V loads target slots that are rewritten
   // before use.)
   if (grp == 0) {
 #pragma unroll
     for (int i = 0; i + 1 < NS; ++i) issue(min(i, last), i, min(i, last), i);
   }
   wait_dma(0);
+  // Every load of this wave has landed, the Q fragments included. Consuming
+  // them here tells the compiler so: it does not see the wait above (inline
+  // assembly), and would otherwise wait for the Q loads, and with them for
+  // every later load of the wave, before the first QK products of each key
+  // block.
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) asm volatile("" ::"v"(qf[kk]));
   lds_barrier();
 
   // VALU step: online softmax of S(j) into P(j). For the FP16 accumulator,
@@ -1065,7 +1198,7 @@ __device__ __forceinline__ FaArgs load_args(uint64_t addr) {
   FaArgs r;
   r.q = a->q;
   r.k = a->k;
-  r.vt = a->vt;
+  r.v = a->v;
   r.o = a->o;
   r.lse = a->lse;
   r.stats = a->stats;
@@ -1086,10 +1219,11 @@ __device__ __forceinline__ FaArgs load_args(uint64_t addr) {
   r.opart = a->opart;
   r.lpart = a->lpart;
   r.splits = a->splits;
+  r.vs = load_strides(a->vs);
   return r;
 }
 
-template <bool ACC16, int BN, int NS, int MODE, bool PACKED>
+template <bool ACC16, int BN, int NS, int MODE, bool PACKED, bool VNAT>
 __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   __shared__ int claimed;
   // Work items: query tiles, or in split mode (tile, part) pairs, the parts
@@ -1113,7 +1247,7 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
     // pressure spills.
     uint64_t addr = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
     asm volatile("" : "+s"(addr));
-    fa_pp_tile<ACC16, BN, NS, MODE, PACKED>(load_args(addr), tile, split);
+    fa_pp_tile<ACC16, BN, NS, MODE, PACKED, VNAT>(load_args(addr), tile, split);
     // Every wave has read `claimed` (and finished with the LDS ring) before
     // thread 0 claims the next tile.
     __syncthreads();
@@ -1121,8 +1255,10 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
 }
 
 // LDS bytes the ping-pong body needs for BN-key blocks (a ring of NS K and
-// NS V^T blocks with padded rows).
-constexpr int pp_lds_bytes(int bn, int ns) { return ns * (bn * (HD * 2 + 16) + HD * (bn * 2 + 16)); }
+// NS V or V^T blocks with padded rows).
+constexpr int pp_lds_bytes(int bn, int ns, bool vnat) {
+  return ns * (k_block_bytes(bn) + v_block_bytes(bn, vnat));
+}
 
 // Device entry points, one per accumulation variant. Their names contain the
 // backend names of the two accumulation variants, which is how a profile
@@ -1131,18 +1267,19 @@ constexpr int pp_lds_bytes(int bn, int ns) { return ns * (bn * (HD * 2 + 16) + H
 // each mode is a separate kernel, so the production kernels carry none of
 // the debug code), PACKED (tiles of packed rows: the group's query heads
 // position by position, see fa_pp_tile; also separate kernels, so the
-// unpacked ones carry none of its row arithmetic). 8 waves of 64 lanes, two
-// per SIMD.
-template <int BN, int NS, int MODE, bool PACKED>
+// unpacked ones carry none of its row arithmetic), VNAT (V read in its
+// natural layout through transposing LDS reads instead of the prep kernel's
+// V^T). 8 waves of 64 lanes, two per SIMD.
+template <int BN, int NS, int MODE, bool PACKED, bool VNAT>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 hip_fa_fp32acc_kernel(FaArgs args) {
-  fa_pp_body<false, BN, NS, MODE, PACKED>(args);
+  fa_pp_body<false, BN, NS, MODE, PACKED, VNAT>(args);
 }
 
-template <int BN, int NS, int MODE, bool PACKED>
+template <int BN, int NS, int MODE, bool PACKED, bool VNAT>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 hip_fa_fp16acc_kernel(FaArgs args) {
-  fa_pp_body<true, BN, NS, MODE, PACKED>(args);
+  fa_pp_body<true, BN, NS, MODE, PACKED, VNAT>(args);
 }
 
 // ----------------------------------------------------------------------------
@@ -1153,6 +1290,7 @@ typedef void (*attn_fn)(FaArgs);
 struct TileConfig {
   const char* name;
   int keys;        // BN
+  bool vnat;       // reads V in its natural layout (no V^T copy)
   int lds;         // dynamic LDS bytes per workgroup
   attn_fn fn[2][2][kModes];   // [packed][acc][mode]
 };
@@ -1160,63 +1298,84 @@ constexpr int kThreads = 512;     // 8 waves
 constexpr int kRows = 256;        // BM: 8 waves x 32 query rows
 constexpr uint64_t kCounterBytes = 256;
 
-#define FA_MODES(KERNEL, BN, NS, PK)                                                        \
-  {&KERNEL<BN, NS, MODE_RUN, PK>, &KERNEL<BN, NS, MODE_CAPTURE, PK>,                         \
-   &KERNEL<BN, NS, MODE_TRACE, PK>, &KERNEL<BN, NS, MODE_SYNC, PK>,                          \
-   &KERNEL<BN, NS, MODE_SPLIT, PK>}
-#define FA_TILE(NAME, BN, NS)                                                               \
+#define FA_MODES(KERNEL, BN, NS, PK, VN)                                                    \
+  {&KERNEL<BN, NS, MODE_RUN, PK, VN>, &KERNEL<BN, NS, MODE_CAPTURE, PK, VN>,                 \
+   &KERNEL<BN, NS, MODE_TRACE, PK, VN>, &KERNEL<BN, NS, MODE_SYNC, PK, VN>,                  \
+   &KERNEL<BN, NS, MODE_SPLIT, PK, VN>}
+#define FA_TILE(NAME, BN, NS, VN)                                                           \
   TileConfig {                                                                              \
-    NAME, BN, pp_lds_bytes(BN, NS), {                                                       \
-      {FA_MODES(hip_fa_fp32acc_kernel, BN, NS, false),                                      \
-       FA_MODES(hip_fa_fp16acc_kernel, BN, NS, false)},                                     \
-      {FA_MODES(hip_fa_fp32acc_kernel, BN, NS, true),                                       \
-       FA_MODES(hip_fa_fp16acc_kernel, BN, NS, true)}                                       \
+    NAME, BN, VN, pp_lds_bytes(BN, NS, VN), {                                               \
+      {FA_MODES(hip_fa_fp32acc_kernel, BN, NS, false, VN),                                  \
+       FA_MODES(hip_fa_fp16acc_kernel, BN, NS, false, VN)},                                 \
+      {FA_MODES(hip_fa_fp32acc_kernel, BN, NS, true, VN),                                   \
+       FA_MODES(hip_fa_fp16acc_kernel, BN, NS, true, VN)}                                   \
     }                                                                                       \
   }
 
 // Every tile masks ragged query and key tails, applies causal masks and has
 // the capture, trace and sync modes.
 const TileConfig kTiles[] = {
-    FA_TILE("pp_n64_r3", 64, 3),      // 64-key blocks, 3-slot LDS ring
-    FA_TILE("pp_n64_r4", 64, 4),      // 64-key blocks, 4-slot LDS ring
-    FA_TILE("pp_n128_r2", 128, 2),    // 128-key blocks, 2-slot LDS ring
+    FA_TILE("pp_n64_r3", 64, 3, false),         // 64-key blocks, 3-slot LDS ring
+    FA_TILE("pp_n64_r4", 64, 4, false),         // 64-key blocks, 4-slot LDS ring
+    FA_TILE("pp_n128_r2", 128, 2, false),       // 128-key blocks, 2-slot LDS ring
+    FA_TILE("pp_n128_r2_vnat", 128, 2, true),   // the same, V read in its natural layout
 };
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
-// Automatic choice (fa_problem.kernel == 0), measured fastest at N = 65536
-// for both accumulators: the 128-key tile.
-constexpr int kAutoFp32 = 3;
-constexpr int kAutoFp16 = 3;
+// Automatic choice (fa_problem.kernel == 0): the 128-key tile, measured
+// fastest at N = 65536 for both accumulators. Its V^T variant runs the key
+// loop about 1.5 % faster (one 16-byte LDS read per PV operand instead of two
+// transposing 8-byte reads); its natural-V variant saves the prep kernel's
+// pass over V (B * Hkv * Nk * 512 bytes of HBM traffic and a launch) and the
+// V^T workspace. The pass costs about 200 / (G * Nq) of the key loop's time
+// (G = Hq / Hkv query heads per KV head), so natural V wins below about
+// 13000 query rows per KV head; the switch sits at kNaturalVRows.
+constexpr int kAutoVt = 3;
+constexpr int kAutoNatural = 4;
+constexpr int64_t kNaturalVRows = 8192;
+
+// Query rows per KV head, or -1 for a geometry validate() rejects.
+int64_t rows_per_kv_head(const fa_problem* p) {
+  if (p->heads_kv <= 0 || p->heads_q <= 0 || p->seq_q <= 0 || p->heads_q % p->heads_kv) return -1;
+  return p->heads_q / p->heads_kv * p->seq_q;
+}
 
 int select_tile(const fa_problem* p, const TileConfig** out) {
   int idx = p->kernel;
-  if (idx == 0) idx = p->acc == FA_ACC_FP16 ? kAutoFp16 : kAutoFp32;
+  if (idx == 0) {
+    const int64_t rows = rows_per_kv_head(p);
+    idx = rows > 0 && rows <= kNaturalVRows ? kAutoNatural : kAutoVt;
+  }
   if (idx < 1 || idx > kNumTiles) return FA_ERR_KERNEL;
   *out = &kTiles[idx - 1];
   return FA_OK;
 }
 
-// Key length of the K and V^T buffers the attention kernel reads: Nk itself
+// Key length of the K and V buffers the attention kernel reads: Nk itself
 // when the tile's key block divides it, else Nk rounded up to a whole block
-// (64 or 128 keys, both multiples of the transpose group), zero-padded by the
-// prep kernel, with the padded K copied into the workspace too. The last
-// block then holds at least one real key.
+// (64 or 128 keys, both whole prep groups), zero-padded by the prep kernel:
+// it then writes padded copies of K and (natural-V tile) V into the
+// workspace. The V^T tiles always read the prep kernel's V^T, the natural-V
+// tile the caller's v (or its padded copy). The last block holds at least
+// one real key.
 struct KeyLayout {
   int64_t nk_pad;
-  bool pad_k;
-  uint64_t vt_bytes, k_bytes;
-  // Workspace: V^T, then the padded K (ragged key tails only), then the
-  // attention kernel's tile counter in a 256-byte slot of its own.
-  uint64_t counter_offset() const { return vt_bytes + k_bytes; }
-  uint64_t workspace_bytes() const { return vt_bytes + k_bytes + kCounterBytes; }
+  bool pad;              // ragged key tail: the kernel reads padded copies
+  bool vnat;             // the tile reads V in its natural layout
+  uint64_t head_bytes;   // one copy of K, V or V^T: B * Hkv * nk_pad * 128 * 2
+  // Workspace: V^T (V^T tiles), the padded K, the padded V (natural-V tile),
+  // then the attention kernel's tile counter in a 256-byte slot of its own.
+  int copies() const { return (vnat ? 0 : 1) + (pad ? (vnat ? 2 : 1) : 0); }
+  uint64_t counter_offset() const { return copies() * head_bytes; }
+  uint64_t workspace_bytes() const { return counter_offset() + kCounterBytes; }
 };
 
 KeyLayout key_layout(const fa_problem* p, const TileConfig* tile) {
   KeyLayout lay;
-  lay.pad_k = p->seq_k % tile->keys != 0;
-  lay.nk_pad = lay.pad_k ? (p->seq_k + tile->keys - 1) / tile->keys * tile->keys : p->seq_k;
-  static_assert(VT_GROUP == 64, "key blocks of 64 and 128 are whole transpose groups");
-  lay.vt_bytes = (uint64_t)p->batch * p->heads_kv * lay.nk_pad * HD * sizeof(_Float16);
-  lay.k_bytes = lay.pad_k ? lay.vt_bytes : 0;
+  lay.pad = p->seq_k % tile->keys != 0;
+  lay.vnat = tile->vnat;
+  lay.nk_pad = lay.pad ? (p->seq_k + tile->keys - 1) / tile->keys * tile->keys : p->seq_k;
+  static_assert(PAD_GROUP == 64, "key blocks of 64 and 128 are whole prep groups");
+  lay.head_bytes = (uint64_t)p->batch * p->heads_kv * lay.nk_pad * HD * sizeof(_Float16);
   return lay;
 }
 
@@ -1241,7 +1400,8 @@ int validate(const fa_problem* p, const TileConfig** tile) {
   const int64_t bh = p->batch * p->heads_q;
   const int64_t tiles_q = (p->seq_q + kRows - 1) / kRows;
   if (bh >= lim || bh * tiles_q >= lim || p->batch * p->heads_kv >= 65536) return FA_ERR_GEOMETRY;
-  // The kernels address a V^T row (Nk' keys) with 32-bit byte offsets.
+  // The kernels address a head's contiguous V^T rows, or its contiguous K
+  // and V rows (Nk' keys), with 32-bit byte offsets.
   if ((int64_t)HD * 2 * key_layout(p, *tile).nk_pad >= ((int64_t)1 << 31)) return FA_ERR_GEOMETRY;
   return FA_OK;
 }
@@ -1396,8 +1556,9 @@ Strides contiguous(int64_t heads, int64_t seq) { return Strides{heads * seq * HD
 Strides strides_of(const int64_t* s) { return Strides{s[0], s[1], s[2]}; }
 
 // Caller strides must keep every 128-element row 16-byte aligned and rows
-// apart (n >= 128); the K rows of one head must span less than 2^31 bytes
-// (32-bit buffer offsets) unless a padded copy of K is read instead.
+// apart (n >= 128); the K rows of one head, and its V rows if the tile reads
+// them in place (natural-V tile), must span less than 2^31 bytes (32-bit
+// buffer offsets) unless padded copies are read instead.
 int check_strides(const fa_problem* p, const fa_strides* s, const KeyLayout& lay) {
   for (const int64_t* t : {s->q, s->k, s->v, s->o})
     for (int i = 0; i < 3; ++i) {
@@ -1406,7 +1567,10 @@ int check_strides(const fa_problem* p, const fa_strides* s, const KeyLayout& lay
     }
   for (const int64_t* t : {s->q, s->k, s->v, s->o})
     if (t[2] < HD) return FA_ERR_GEOMETRY;
-  if (!lay.pad_k && (p->seq_k - 1) * s->k[2] * 2 + HD * 2 >= ((int64_t)1 << 31)) return FA_ERR_GEOMETRY;
+  if (!lay.pad)
+    for (const int64_t* t : {s->k, s->v})
+      if ((t == s->k || lay.vnat) && (p->seq_k - 1) * t[2] * 2 + HD * 2 >= ((int64_t)1 << 31))
+        return FA_ERR_GEOMETRY;
   return FA_OK;
 }
 
@@ -1514,14 +1678,18 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
   }
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  _Float16* vt = static_cast<_Float16*>(workspace);
-  _Float16* kpad = lay.pad_k ? vt + lay.vt_bytes / sizeof(_Float16) : nullptr;
+  // Workspace: [V^T] [padded K] [padded V] counter, as the layout has them.
+  _Float16* ws = static_cast<_Float16*>(workspace);
+  const uint64_t head_elems = lay.head_bytes / sizeof(_Float16);
+  _Float16* vt = lay.vnat ? nullptr : ws;
+  _Float16* kpad = lay.pad ? ws + (lay.vnat ? 0 : head_elems) : nullptr;
+  _Float16* vpad = lay.pad && lay.vnat ? kpad + head_elems : nullptr;
   int* next_tile = reinterpret_cast<int*>(static_cast<char*>(workspace) + lay.counter_offset());
 
   // hipLaunchKernel returns the status of this launch alone; errors left
   // pending by the caller's earlier work are neither read nor cleared.
   if (mode == MODE_SYNC) {
-    // Sync mode: the workspace (V^T, padded K) starts as FP16 NaN, so a read
+    // Sync mode: the workspace (V^T, padded K and V) starts as FP16 NaN, so a read
     // of any element the prep kernel does not write reaches the output.
     u32x4* ws = static_cast<u32x4*>(workspace);
     uint64_t n16 = lay.counter_offset() / 16;
@@ -1535,17 +1703,21 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
     const _Float16* kk = static_cast<const _Float16*>(k);
     const _Float16* vv = static_cast<const _Float16*>(v);
     int nk_valid = (int)p->seq_k, nk_pad = (int)lay.nk_pad, heads_kv = (int)p->heads_kv;
-    void* prep_args[] = {&kk, &vv, &vt, &kpad, &nk_valid, &nk_pad, &heads_kv, &ks, &vs, &next_tile};
-    const dim3 prep_grid((unsigned)(lay.nk_pad / VT_GROUP), (unsigned)(p->batch * p->heads_kv));
-    if (hipLaunchKernel(reinterpret_cast<const void*>(&fa_prep_kernel), prep_grid, dim3(256),
-                        prep_args, 0, st) != hipSuccess)
-      return FA_ERR_LAUNCH;
+    void* vt_args[] = {&kk, &vv, &vt, &kpad, &nk_valid, &nk_pad, &heads_kv, &ks, &vs, &next_tile};
+    void* pad_args[] = {&kk, &vv, &kpad, &vpad, &nk_valid, &nk_pad, &heads_kv, &ks, &vs, &next_tile};
+    const dim3 groups((unsigned)(lay.nk_pad / PAD_GROUP), (unsigned)(p->batch * p->heads_kv));
+    const bool ok = lay.vnat ? hipLaunchKernel(reinterpret_cast<const void*>(&fa_pad_kernel),
+                                               lay.pad ? groups : dim3(1, 1), dim3(256), pad_args,
+                                               0, st) == hipSuccess
+                             : hipLaunchKernel(reinterpret_cast<const void*>(&fa_prep_kernel), groups,
+                                               dim3(256), vt_args, 0, st) == hipSuccess;
+    if (!ok) return FA_ERR_LAUNCH;
   }
 
   FaArgs args;
   args.q = static_cast<const _Float16*>(q);
-  args.k = lay.pad_k ? kpad : static_cast<const _Float16*>(k);
-  args.vt = vt;
+  args.k = lay.pad ? kpad : static_cast<const _Float16*>(k);
+  args.v = !lay.vnat ? vt : lay.pad ? vpad : static_cast<const _Float16*>(v);
   args.o = static_cast<_Float16*>(o);
   args.lse = ex.lse;
   args.stats = ex.stats;
@@ -1565,7 +1737,8 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
   args.c = (float)((double)p->scale * LOG2E);
   args.qs = qs;
   args.os = os;
-  args.ks = lay.pad_k ? contiguous(p->heads_kv, lay.nk_pad) : ks;
+  args.ks = lay.pad ? contiguous(p->heads_kv, lay.nk_pad) : ks;
+  args.vs = lay.pad || !lay.vnat ? contiguous(p->heads_kv, lay.nk_pad) : vs;
   void* attn_args[] = {&args};
   // One workgroup per CU (the LDS ring leaves room for no second one), never
   // more workgroups than work items.

@@ -21,6 +21,16 @@
  * row's result is the same bit for bit either way; packing only lets the
  * heads that share K and V share a tile.
  *
+ * V layouts: the 128-key tile comes in two forms with identical results bit
+ * for bit. pp_n128_r2 (and the 64-key tiles) read V^T, a key-permuted
+ * transposed copy of v that a prep kernel writes into the workspace before
+ * the attention kernel runs; pp_n128_r2_vnat reads v where it lies, through
+ * gfx950's transposing LDS reads, with no prep pass over v and no V^T in the
+ * workspace, and runs its key loop about 1.5 % slower. The automatic choice
+ * takes pp_n128_r2_vnat for at most 8192 query rows per KV head
+ * ((Hq / Hkv) * Nq: decode, short prompts against long keys), where the
+ * prep pass would cost more, and pp_n128_r2 otherwise.
+ *
  * Conventions (mirroring the reference's two-phase operator binding):
  *   - every entry point returns 0 on success and a nonzero FA_ERR_* code
  *     otherwise; fa_strerror() names the code;
@@ -103,10 +113,13 @@ typedef struct fa_problem {
 } fa_problem;
 
 /*
- * Bytes of device workspace fa_fwd() needs for problem *p (the key-permuted
- * transposed copy of v; with a ragged key tail, zero-padded copies of k and
- * v^T to a whole key block of the selected tile; 256 bytes for the counter
- * the kernel's workgroups take query tiles from). Replaces phase 1 of the
+ * Bytes of device workspace fa_fwd() needs for problem *p: 256 bytes for the
+ * counter the kernel's workgroups take query tiles from, plus, for a tile
+ * that reads V^T (see V layouts above), V^T (B * Hkv * Nk' * 256 bytes), and,
+ * with a ragged key tail, zero-padded copies to a whole key block of the
+ * selected tile (Nk' keys) of k (V^T tiles) or of k and v (pp_n128_r2_vnat),
+ * B * Hkv * Nk' * 256 bytes each. pp_n128_r2_vnat without a key tail reads k
+ * and v where they lie and needs the 256-byte counter alone. Replaces phase 1 of the
  * reference's operator call,
  * aclnn<Op>GetWorkspaceSize (backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/
  * binding.py:21-24,74-75), whose host tiling sizes the scratch buffer
@@ -213,7 +226,7 @@ int fa_fwd_trace(const fa_problem* p, const void* q, const void* k, const void* 
  * Synchronous debug mode: fa_fwd_lse() (lse may be NULL) through a separate
  * instantiation of the same tile that removes the overlap of loads and
  * compute and poisons every buffer the kernels stage through: the workspace
- * (V^T, padded K) is filled with FP16 NaN before the prep kernel rewrites
+ * (padded K and V) is filled with FP16 NaN before the prep kernel rewrites
  * it, each query tile fills its whole LDS ring (row pads included) with NaN
  * before its first load, and the loads of each phase complete before that
  * phase ends instead of one phase later. A read of staging memory that no
@@ -257,12 +270,14 @@ const char* fa_kernel_name(int32_t kernel);
  * fa_fwd() without a caller workspace, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference. The
- * workspace (the transposed V and, with a ragged key tail, padded K and V^T)
- * lives in a static device array of FA_NOALLOC_SCRATCH_BYTES per GPU, which
- * the library holds from module load until the process ends; problems whose
- * fa_fwd_workspace_bytes() exceeds it fail with FA_ERR_SCRATCH before any
- * work is enqueued (64 MiB + 64 KiB covers e.g. B * Hkv * Nk = 2 * 131072
- * keys with no key tail, the B=2 N=131072 configuration). Nothing is allocated or freed:
+ * workspace (fa_fwd_workspace_bytes(): the tile counter, V^T for the V^T
+ * tiles, padded copies for a ragged key tail) lives in a static device array
+ * of FA_NOALLOC_SCRATCH_BYTES per GPU, which the library holds from module
+ * load until the process ends; problems whose fa_fwd_workspace_bytes()
+ * exceeds it fail with FA_ERR_SCRATCH before any work is enqueued (64 MiB +
+ * 64 KiB covers B * Hkv * Nk' = 131072 keys of V^T, e.g. the B=2 N=131072
+ * configuration, and every problem pp_n128_r2_vnat runs without a key
+ * tail). Nothing is allocated or freed:
  * the first call on a device looks up that device's array address
  * (hipGetSymbolAddress) and keeps it. Every call on one GPU shares that
  * array and each call overwrites what it uses, so calls that overlap on one

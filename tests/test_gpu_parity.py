@@ -320,11 +320,11 @@ def kernel_ids():
 
 def tile_of(kernel):
     """(query rows, keys) of one workgroup block of tile configuration ``kernel``,
-    from its name pp_n{keys}_r{ring}: 256 query rows per workgroup."""
+    from its name pp_n{keys}_r{ring}[_vnat]: 256 query rows per workgroup."""
     from fa_amd import binding, build
 
     name = binding.load_library(build.LIBRARY).fa_kernel_name(kernel).decode()
-    parts = dict((p[0], int(p[1:])) for p in name.split("_")[1:])
+    parts = dict((p[0], int(p[1:])) for p in name.split("_")[1:] if p[1:].isdigit())
     return 256, parts["n"]
 
 

@@ -50,11 +50,24 @@ def lib(library_path):
 
 
 def test_workspace_size(lib):
-    # V^T, plus 256 bytes for the work-queue counter.
+    # Many query rows per KV head (12 x 4096): the V^T tile, whose workspace
+    # holds V^T, plus 256 bytes for the work-queue counter.
     rc, size = ws_bytes(lib, problem(batch=2, heads_kv=1, seq_k=131072))
     assert rc == 0 and size == 2 * 1 * 131072 * 128 * 2 + 256
+    # A ragged key tail adds the zero-padded K.
+    rc, size = ws_bytes(lib, problem(seq_k=1000))
+    assert rc == 0 and size == 2 * 1024 * 128 * 2 + 256
+    # Few query rows per KV head (2 x 512): the natural-V tile reads K and V
+    # where they lie, so only the counter.
     rc, size = ws_bytes(lib, problem(heads_q=8, heads_kv=4, seq_q=512, seq_k=1024))
-    assert rc == 0 and size == 4 * 1024 * 128 * 2 + 256
+    assert rc == 0 and size == 256
+    # A ragged key tail adds zero-padded copies of K and V for every KV head.
+    rc, size = ws_bytes(lib, problem(heads_q=8, heads_kv=4, seq_q=512, seq_k=1000))
+    assert rc == 0 and size == 2 * 4 * 1024 * 128 * 2 + 256
+    # Forcing either tile gives its own layout whatever the shape.
+    assert ws_bytes(lib, problem(batch=2, seq_k=131072, kernel=4)) == (0, 256)
+    assert ws_bytes(lib, problem(heads_q=8, heads_kv=4, seq_q=512, seq_k=1024, kernel=3)) == \
+        (0, 4 * 1024 * 128 * 2 + 256)
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -71,15 +84,18 @@ def test_geometry_errors(lib, kw, code):
 
 def test_ragged_tails_and_workspace(lib):
     # The automatic choice masks ragged tails, so any Nq, Nk >= 1 is valid;
-    # a ragged key tail adds zero-padded copies of K and V^T (whole blocks of
-    # the FP32 default tile: 128 keys).
+    # a ragged key tail adds zero-padded copies (whole blocks of the 128-key
+    # tile): of K and V for the natural-V tile (few query rows per KV head),
+    # of K beside V^T for the V^T tile (many), two copies either way.
     for nq, nk in ((1, 1), (300, 1000), (4097, 4095), (256, 129)):
         rc, size = ws_bytes(lib, problem(seq_q=nq, seq_k=nk))
         assert rc == 0, (nq, nk)
         pad = -(-nk // 128) * 128
         assert size == 2 * pad * 128 * 2 + 256, (nq, nk, size)
     rc, size = ws_bytes(lib, problem(seq_q=300, seq_k=4096))
-    assert rc == 0 and size == 4096 * 128 * 2 + 256    # no key tail: V^T only
+    assert rc == 0 and size == 256                     # natural V, no key tail: the counter
+    rc, size = ws_bytes(lib, problem(seq_q=4096, seq_k=4096))
+    assert rc == 0 and size == 4096 * 128 * 2 + 256    # V^T, no key tail: V^T and the counter
     # A 64-key tile pads to whole 64-key blocks.
     rc, size = ws_bytes(lib, problem(seq_q=300, seq_k=1000, kernel=1))
     assert rc == 0 and size == 2 * 1024 * 128 * 2 + 256
@@ -109,7 +125,7 @@ def test_causal_selection(lib):
 
 
 def test_key_length_limit(lib):
-    # V^T rows are addressed with 32-bit byte offsets: 128 rows x Nk' keys x 2 B < 2^31.
+    # A head's K and V rows are addressed with 32-bit byte offsets: Nk' keys x 256 B < 2^31.
     assert ws_bytes(lib, problem(seq_q=256, seq_k=8_000_000))[0] == 0
     assert ws_bytes(lib, problem(seq_q=256, seq_k=9_000_000))[0] == 2
 
@@ -210,7 +226,7 @@ def test_fwd_rejects_before_launch(lib):
 
 def test_kernel_table(lib):
     n = lib.fa_kernel_count()
-    assert n == 3
+    assert n == 4
     names = [lib.fa_kernel_name(i).decode() for i in range(1, n + 1)]
     assert len(set(names)) == n
     assert lib.fa_kernel_name(0) is None and lib.fa_kernel_name(n + 1) is None
@@ -227,13 +243,18 @@ def test_kernel_table(lib):
 
 
 def test_automatic_choice(lib):
-    # kernel = 0: the 128-key tile for both accumulators.
+    # kernel = 0: the 128-key tile for both accumulators, reading V^T with
+    # more than 8192 query rows per KV head (group x Nq) and V in its
+    # natural layout with at most that many.
     sel = C.c_int32()
-    for seq in (4096, 131072, 1000):
+    cases = [(12, 1, 4096, b"pp_n128_r2"), (12, 1, 131072, b"pp_n128_r2"), (12, 1, 1000, b"pp_n128_r2"),
+             (12, 1, 683, b"pp_n128_r2"), (12, 1, 682, b"pp_n128_r2_vnat"), (12, 1, 1, b"pp_n128_r2_vnat"),
+             (8, 8, 8192, b"pp_n128_r2_vnat"), (8, 8, 8193, b"pp_n128_r2"), (64, 8, 1, b"pp_n128_r2_vnat")]
+    for hq, hkv, seq, name in cases:
         for acc in (0, 1):
-            prob = problem(seq_q=seq, seq_k=seq, acc=acc)
+            prob = problem(heads_q=hq, heads_kv=hkv, seq_q=seq, seq_k=seq, acc=acc)
             assert lib.fa_fwd_select(C.byref(prob), C.byref(sel)) == 0
-            assert lib.fa_kernel_name(sel.value) == b"pp_n128_r2"
+            assert lib.fa_kernel_name(sel.value) == name, (hq, hkv, seq)
 
 
 def test_operator_validation_without_gpu(library_path):
@@ -274,14 +295,18 @@ def test_strided_validation(lib):
     assert call(k=(256 * 128, -8, 128)) == 2                     # negative stride
     assert call(o=(4 * 256 * 128, 256 * 128, 64)) == 2           # rows overlap
     assert call(k=(0, 0, 1 << 23), v=(0, 0, 128)) == 2           # key rows span >= 2^31 bytes
+    assert call(v=(0, 0, 1 << 23)) == 2                          # so do the value rows
 
 
 def test_noalloc_rejects_before_touching_the_gpu(lib):
     # Problems whose workspace exceeds the static scratch (64 MiB) and NULL
-    # tensors are refused on the host.
+    # tensors are refused on the host. A ragged key tail needs padded copies
+    # of K and V: 2 * 4 * 131072 keys * 256 B = 256 MiB here.
     fake = C.c_void_p(4096)
-    big = problem(batch=4, seq_q=256, seq_k=131072)          # 4 * 131072 keys * 256 B = 128 MiB
+    big = problem(batch=4, seq_q=256, seq_k=131071)
     assert lib.fa_fwd_noalloc(C.byref(big), fake, fake, fake, fake, None) == 14
+    rc, size = ws_bytes(lib, problem(batch=4, seq_q=256, seq_k=131072))   # no tail: the counter
+    assert rc == 0 and size == 256
     assert lib.fa_fwd_noalloc(C.byref(problem(dim=64)), fake, fake, fake, fake, None) == 3
     assert lib.fa_fwd_noalloc(C.byref(problem()), None, fake, fake, fake, None) == 1
     assert lib.fa_fwd_noalloc(None, fake, fake, fake, fake, None) == 1

@@ -3,8 +3,8 @@
 Its workspace is the library's static device array (FA_NOALLOC_SCRATCH_BYTES
 per GPU). Called through the C ABI, it must give exactly fa_fwd's output (the
 same kernels, only the workspace differs), on two calls in a row, the second
-with a smaller input (a ragged one, which also uses the padded-K part of the
-scratch), and refuse problems whose workspace exceeds the array before any
+with a smaller input (a ragged one, which also uses the padded K and V
+copies in the scratch), and refuse problems whose workspace exceeds the array before any
 work is enqueued.
 """
 
@@ -73,7 +73,7 @@ def test_noalloc_headline_size_fits_and_oversize_is_refused(library_path):
     c3 = binding.FaProblem(2, 12, 1, 131072, 131072, 128, 128 ** -0.5, 0, 0, 0)
     assert lib.fa_fwd_workspace_bytes(C.byref(c3), C.byref(size)) == 0
     assert size.value <= binding.NOALLOC_SCRATCH_BYTES
-    big = binding.FaProblem(4, 12, 1, 256, 131072, 128, 128 ** -0.5, 0, 0, 0)
+    big = binding.FaProblem(4, 12, 1, 256, 131071, 128, 128 ** -0.5, 0, 0, 0)   # ragged: 256 MiB
     fake = C.c_void_p(4096)
     assert lib.fa_fwd_noalloc(C.byref(big), fake, fake, fake, fake, None) == 14
     assert b"scratch" in lib.fa_strerror(14)

@@ -1063,7 +1063,48 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
   // group 0. The wave that issues a pair's loads also waits for them, at the
   // end of the phase before the loaded blocks are read.
   constexpr bool LOADS_IN_VALU = !ACC16;
-  if (grp == 0) {
+  // A wave whose 32 rows all lie past the row sequence (in a ragged last
+  // tile, or a packed decode tile of a few rows) computes nothing anyone
+  // reads: it skips its MFMA and VALU steps but issues its share of every
+  // pair's loads, in the phase its group issues them, waits for them where
+  // its group does and passes the same 2 * nblk + 2 barriers, so the ring
+  // schedule is that of the full tile. The other wave of its SIMD then runs
+  // its steps alone. Wave 0 always holds a row.
+  const bool idle = qt * BM + wave_u * 32 >= seq_r;
+  if (idle) {
+    if (grp == 0) {
+      for (int j = 0; j < nblk; ++j) {
+        const int sp = prev(sl);
+        if constexpr (!LOADS_IN_VALU) {           // phase 2j: pair j's loads
+          issue(min(j + NS - 1, last), sp, min(j + NS - 2, last), prev(sp));
+          if constexpr (SYNC) wait_dma(0);
+        }
+        lds_barrier();
+        if constexpr (!LOADS_IN_VALU) wait_dma(keep);   // phase 2j + 1
+        lds_barrier();
+        sl = next(sl);
+      }
+      lds_barrier();                           // phase 2 nblk
+      lds_barrier();                           // phase 2 nblk + 1
+    } else {
+      if constexpr (LOADS_IN_VALU) {           // phase 0: pair 0's loads
+        issue(min(NS - 1, last), NS - 1, min(NS - 2, last), NS - 2);
+        if constexpr (SYNC) wait_dma(0);
+      }
+      lds_barrier();
+      for (int j = 0; j < nblk; ++j) {
+        if constexpr (LOADS_IN_VALU) wait_dma(keep);   // phase 2j + 1
+        lds_barrier();
+        if constexpr (LOADS_IN_VALU) {         // phase 2j + 2: pair j + 1's loads
+          issue(min(j + NS, last), sl, min(j + NS - 1, last), prev(sl));
+          if constexpr (SYNC) wait_dma(0);
+        }
+        lds_barrier();
+        sl = next(sl);
+      }
+      lds_barrier();                           // phase 2 nblk + 1
+    }
+  } else if (grp == 0) {
     auto pair = [&](int j, auto mask) {
       const int sp = prev(sl);
       mfma_step(kslot(sl), vslot(sp), !LOADS_IN_VALU, min(j + NS - 1, last), sp,

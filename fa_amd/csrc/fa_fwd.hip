@@ -1364,15 +1364,18 @@ const TileConfig kTiles[] = {
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 // Automatic choice (fa_problem.kernel == 0): the 128-key tile, measured
 // fastest at N = 65536 for both accumulators. Its V^T variant runs the key
-// loop about 1.5 % faster (one 16-byte LDS read per PV operand instead of two
-// transposing 8-byte reads); its natural-V variant saves the prep kernel's
-// pass over V (B * Hkv * Nk * 512 bytes of HBM traffic and a launch) and the
-// V^T workspace. The pass costs about 200 / (G * Nq) of the key loop's time
-// (G = Hq / Hkv query heads per KV head), so natural V wins below about
-// 13000 query rows per KV head; the switch sits at kNaturalVRows.
+// loop faster (one 16-byte LDS read per PV operand instead of two
+// transposing 8-byte reads: 1.5 % at B=2 N=131072, 4-12 % on shorter or
+// many-KV-head problems); its natural-V variant saves the prep kernel's pass
+// over V (B * Hkv * Nk * 512 bytes of HBM traffic and a launch) and the V^T
+// workspace, which matters when there is little attention work per key:
+// few query rows per KV head (G * Nq, G = Hq / Hkv). Timed against each
+// other (automatic split count, one session), natural V was 5 % faster at
+// 1536 rows per KV head and 4-12 % slower from 3072 up; the switch sits at
+// kNaturalVRows.
 constexpr int kAutoVt = 3;
 constexpr int kAutoNatural = 4;
-constexpr int64_t kNaturalVRows = 8192;
+constexpr int64_t kNaturalVRows = 2048;
 
 // Query rows per KV head, or -1 for a geometry validate() rejects.
 int64_t rows_per_kv_head(const fa_problem* p) {

@@ -5,7 +5,7 @@ with fewer tiles than the GPU has CUs (a short query range or a small batch
 against long keys) leaves CUs idle for its whole duration. The key-split
 forward (``fa_fwd_split``) cuts every tile's key range into parts, runs each
 (tile, part) as its own work item and merges the parts' (O, lse) pairs. For
-each shape this prints the library's automatic part count, the device time
+each shape this prints the library's automatic tile and part count, the device time
 per forward of both paths (HIP events around ``--steps`` forwards after
 ``--warmup``), the achieved QK/PV TFLOP/s (4 B Hq Nq Nk 128 FLOP) and the
 largest difference between the two outputs. With ``--sweep`` it times the
@@ -24,11 +24,13 @@ import sys
 # (B, Hq, Hkv, Nq, Nk): the headline's head layout with short query ranges
 # against long keys, one or a few query rows per head (decode: the group's
 # heads share one packed tile), a batched decode with 8 KV heads of 8 query
-# heads each, and c0 (B1 N4096).
+# heads each, and c0 (B1 N4096). Up to 128 query rows per head (1536 per KV
+# head) the automatic tile reads V in its natural layout.
 SHAPES = [
     (1, 12, 1, 1, 131072),
     (1, 12, 1, 16, 131072),
     (8, 64, 8, 1, 8192),
+    (1, 12, 1, 128, 131072),
     (1, 12, 1, 256, 131072),
     (1, 12, 1, 1024, 131072),
     (1, 12, 1, 4096, 131072),
@@ -77,6 +79,7 @@ def measure(shape, acc, warmup, steps, seed=0):
     diff = float((one(q, k, v).float() - split(q, k, v).float()).abs().max())
     return {
         "shape": shape, "parts": split.split_count(q.shape, k.shape),
+        "tile": split.kernel_name(q.shape, k.shape),
         "one_us": us_one, "split_us": us_split,
         "one_tflops": flops / us_one / 1e6, "split_tflops": flops / us_split / 1e6,
         "max_diff": diff,
@@ -114,16 +117,16 @@ def render_sweep(rows, acc, command):
 
 
 def render(rows, acc, command):
-    lines = [f"# one-pass vs key-split forward, hip_fa_{acc}acc (automatic part count), one MI355X",
+    lines = [f"# one-pass vs key-split forward, hip_fa_{acc}acc (automatic tile and part count), one MI355X",
              f"command: {command}",
-             f"{'B,Hq,Hkv,Nq,Nk':<22} {'tiles':>5} {'parts':>5} {'one-pass us':>12} {'TFLOP/s':>8} "
+             f"{'B,Hq,Hkv,Nq,Nk':<22} {'tile':<16} {'tiles':>5} {'parts':>5} {'one-pass us':>12} {'TFLOP/s':>8} "
              f"{'split us':>10} {'TFLOP/s':>8} {'speedup':>7} {'max|diff|':>10}"]
     from fa_amd import binding
 
     for r in rows:
         b, hq, hkv, nq, _ = r["shape"]
         tiles = binding.query_tiles(b, hq, hkv, nq)
-        lines.append(f"{','.join(map(str, r['shape'])):<22} {tiles:>5} {r['parts']:>5} "
+        lines.append(f"{','.join(map(str, r['shape'])):<22} {r['tile']:<16} {tiles:>5} {r['parts']:>5} "
                      f"{r['one_us']:>12.1f} {r['one_tflops']:>8.1f} {r['split_us']:>10.1f} "
                      f"{r['split_tflops']:>8.1f} {r['one_us'] / r['split_us']:>6.2f}x "
                      f"{r['max_diff']:>10.2e}")

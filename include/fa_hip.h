@@ -26,10 +26,10 @@
  * transposed copy of v that a prep kernel writes into the workspace before
  * the attention kernel runs; pp_n128_r2_vnat reads v where it lies, through
  * gfx950's transposing LDS reads, with no prep pass over v and no V^T in the
- * workspace, and runs its key loop about 1.5 % slower. The automatic choice
- * takes pp_n128_r2_vnat for at most 8192 query rows per KV head
- * ((Hq / Hkv) * Nq: decode, short prompts against long keys), where the
- * prep pass would cost more, and pp_n128_r2 otherwise.
+ * workspace, and runs its key loop 1.5-12 % slower. The automatic choice
+ * takes pp_n128_r2_vnat for at most 2048 query rows per KV head
+ * ((Hq / Hkv) * Nq: decode and other short query ranges against long keys),
+ * where the prep pass costs more, and pp_n128_r2 otherwise.
  *
  * Conventions (mirroring the reference's two-phase operator binding):
  *   - every entry point returns 0 on success and a nonzero FA_ERR_* code

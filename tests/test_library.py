@@ -92,7 +92,7 @@ def test_ragged_tails_and_workspace(lib):
         assert rc == 0, (nq, nk)
         pad = -(-nk // 128) * 128
         assert size == 2 * pad * 128 * 2 + 256, (nq, nk, size)
-    rc, size = ws_bytes(lib, problem(seq_q=300, seq_k=4096))
+    rc, size = ws_bytes(lib, problem(seq_q=100, seq_k=4096))
     assert rc == 0 and size == 256                     # natural V, no key tail: the counter
     rc, size = ws_bytes(lib, problem(seq_q=4096, seq_k=4096))
     assert rc == 0 and size == 4096 * 128 * 2 + 256    # V^T, no key tail: V^T and the counter
@@ -244,12 +244,12 @@ def test_kernel_table(lib):
 
 def test_automatic_choice(lib):
     # kernel = 0: the 128-key tile for both accumulators, reading V^T with
-    # more than 8192 query rows per KV head (group x Nq) and V in its
+    # more than 2048 query rows per KV head (group x Nq) and V in its
     # natural layout with at most that many.
     sel = C.c_int32()
     cases = [(12, 1, 4096, b"pp_n128_r2"), (12, 1, 131072, b"pp_n128_r2"), (12, 1, 1000, b"pp_n128_r2"),
-             (12, 1, 683, b"pp_n128_r2"), (12, 1, 682, b"pp_n128_r2_vnat"), (12, 1, 1, b"pp_n128_r2_vnat"),
-             (8, 8, 8192, b"pp_n128_r2_vnat"), (8, 8, 8193, b"pp_n128_r2"), (64, 8, 1, b"pp_n128_r2_vnat")]
+             (12, 1, 171, b"pp_n128_r2"), (12, 1, 170, b"pp_n128_r2_vnat"), (12, 1, 1, b"pp_n128_r2_vnat"),
+             (8, 8, 2048, b"pp_n128_r2_vnat"), (8, 8, 2049, b"pp_n128_r2"), (64, 8, 16, b"pp_n128_r2_vnat")]
     for hq, hkv, seq, name in cases:
         for acc in (0, 1):
             prob = problem(heads_q=hq, heads_kv=hkv, seq_q=seq, seq_k=seq, acc=acc)
@@ -300,12 +300,12 @@ def test_strided_validation(lib):
 
 def test_noalloc_rejects_before_touching_the_gpu(lib):
     # Problems whose workspace exceeds the static scratch (64 MiB) and NULL
-    # tensors are refused on the host. A ragged key tail needs padded copies
-    # of K and V: 2 * 4 * 131072 keys * 256 B = 256 MiB here.
+    # tensors are refused on the host: here V^T and a padded K, 2 * 4 *
+    # 131072 keys * 256 B = 256 MiB.
     fake = C.c_void_p(4096)
     big = problem(batch=4, seq_q=256, seq_k=131071)
     assert lib.fa_fwd_noalloc(C.byref(big), fake, fake, fake, fake, None) == 14
-    rc, size = ws_bytes(lib, problem(batch=4, seq_q=256, seq_k=131072))   # no tail: the counter
+    rc, size = ws_bytes(lib, problem(batch=4, seq_q=16, seq_k=131072))   # natural V: the counter
     assert rc == 0 and size == 256
     assert lib.fa_fwd_noalloc(C.byref(problem(dim=64)), fake, fake, fake, fake, None) == 3
     assert lib.fa_fwd_noalloc(C.byref(problem()), None, fake, fake, fake, None) == 1

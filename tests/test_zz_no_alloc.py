@@ -3,8 +3,8 @@
 Its workspace is the library's static device array (FA_NOALLOC_SCRATCH_BYTES
 per GPU). Called through the C ABI, it must give exactly fa_fwd's output (the
 same kernels, only the workspace differs), on two calls in a row, the second
-with a smaller input (a ragged one, which also uses the padded K and V
-copies in the scratch), and refuse problems whose workspace exceeds the array before any
+with a smaller input (ragged ones, which also use the padded copies in the
+scratch, through both V layouts), and refuse problems whose workspace exceeds the array before any
 work is enqueued.
 """
 
@@ -56,7 +56,10 @@ def without_workspace(lib, prob, q, k, v):
 @pytest.mark.parametrize("acc", [0, 1])
 def test_noalloc_matches_fa_fwd_on_two_calls(library_path, acc):
     lib = binding.load_library(library_path)
-    shapes = [(2, 12, 1, 4096, 4096), (1, 6, 2, 700, 1000)]     # second call: smaller, ragged
+    # Second call smaller and ragged (V^T and a padded K in the scratch);
+    # third smaller still, few query rows per KV head (the natural-V tile:
+    # padded K and V copies in the scratch).
+    shapes = [(2, 12, 1, 4096, 4096), (1, 6, 2, 700, 1000), (1, 8, 2, 100, 999)]
     for i, (b, hq, hkv, nq, nk) in enumerate(shapes):
         say(f"case noalloc acc={acc} call {i}: B={b} Hq={hq} Hkv={hkv} Nq={nq} Nk={nk}")
         q, k, v = inputs(b, hq, hkv, nq, nk, seed=10 * i + acc)

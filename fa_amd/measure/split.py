@@ -87,7 +87,8 @@ def measure(shape, acc, warmup, steps, seed=0):
 
 
 def sweep(shape, acc, warmup, steps, seed=0):
-    """(automatic count, [(count, device us)]) over SWEEP_COUNTS."""
+    """(automatic count, [(count, device us)]) over SWEEP_COUNTS and the
+    automatic count."""
     from fa_amd import build
     from fa_amd.binding import AttentionConfig, Operator
     from fa_amd.harness import timing
@@ -95,7 +96,7 @@ def sweep(shape, acc, warmup, steps, seed=0):
     q, k, v = _inputs(shape, seed)
     auto = Operator(build.LIBRARY, AttentionConfig(acc=acc, splits=0)).split_count(q.shape, k.shape)
     res = []
-    for n in SWEEP_COUNTS:
+    for n in sorted(set(SWEEP_COUNTS) | {auto}):
         if n > -(-shape[4] // 128):
             continue
         op = Operator(build.LIBRARY, AttentionConfig(acc=acc, splits=n))

@@ -144,12 +144,16 @@ def test_split_table_render():
     assert split.parse_shape("1,12,1,256,131072") == (1, 12, 1, 256, 131072)
     with pytest.raises(Exception):
         split.parse_shape("1,12,1")
-    rows = [{"shape": (1, 12, 1, 256, 131072), "parts": 21, "one_us": 2149.0, "split_us": 224.0,
-             "one_tflops": 95.9, "split_tflops": 920.3, "max_diff": 1.2e-4}]
+    rows = [{"shape": (1, 12, 1, 256, 131072), "parts": 21, "tile": "pp_n128_r2", "one_us": 2149.0,
+             "split_us": 224.0, "one_tflops": 95.9, "split_tflops": 920.3, "max_diff": 1.2e-4},
+            {"shape": (1, 12, 1, 1, 131072), "parts": 256, "tile": "pp_n128_r2_vnat", "one_us": 1511.0,
+             "split_us": 27.7, "one_tflops": 0.5, "split_tflops": 29.1, "max_diff": 7.6e-6}]
     lines = split.render(rows, "fp32", "python -m fa_amd.measure.split")
     assert lines[1] == "command: python -m fa_amd.measure.split"
     row = lines[3].split()
-    assert row[:3] == ["1,12,1,256,131072", "12", "21"] and row[7] == "9.59x"
+    assert row[:4] == ["1,12,1,256,131072", "pp_n128_r2", "12", "21"] and row[8] == "9.59x"
+    row = lines[4].split()      # decode: one packed tile
+    assert row[:4] == ["1,12,1,1,131072", "pp_n128_r2_vnat", "1", "256"] and row[8] == "54.55x"
 
 
 def test_split_sweep_render():

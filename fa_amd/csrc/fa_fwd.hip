@@ -1227,7 +1227,10 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
 // launch ends with the slowest one, while from a shared counter the faster
 // dies take more tiles. Every workgroup leaves once the counter passes the
 // tile count, so the grid drains. The counter lives in the workspace and is
-// zeroed by the prep kernel, which runs first on the same stream.
+// zeroed by the prep kernel, which runs first on the same stream. A launch
+// with no more work items than CUs has one workgroup per item (the grid is
+// never larger than the item count), and then each workgroup takes item
+// blockIdx.x without the counter, so such a launch needs no counter reset.
 // Copy of the kernel arguments read from the kernel-argument segment at
 // address `addr` (scalar loads), field by field.
 typedef const FaArgs __attribute__((address_space(4)))* KernargArgs;
@@ -1271,10 +1274,15 @@ __device__ __forceinline__ void fa_pp_body(const FaArgs& args) {
   // of one tile consecutive.
   int items = args.tiles;
   if constexpr (MODE == MODE_SPLIT) items *= args.splits;
-  for (;;) {
-    if (threadIdx.x == 0) claimed = atomicAdd(args.next_tile, 1);
+  const bool direct = items <= (int)gridDim.x;   // one workgroup per item
+  for (int n = 0;; ++n) {
+    if (direct) {
+      if (n > 0) break;
+    } else if (threadIdx.x == 0) {
+      claimed = atomicAdd(args.next_tile, 1);
+    }
     __syncthreads();
-    const int item = __builtin_amdgcn_readfirstlane(claimed);
+    const int item = direct ? (int)blockIdx.x : __builtin_amdgcn_readfirstlane(claimed);
     if (item >= items) break;
     int tile = item, split = 0;
     if constexpr (MODE == MODE_SPLIT) {
@@ -1750,11 +1758,17 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
     void* vt_args[] = {&kk, &vv, &vt, &kpad, &nk_valid, &nk_pad, &heads_kv, &ks, &vs, &next_tile};
     void* pad_args[] = {&kk, &vv, &kpad, &vpad, &nk_valid, &nk_pad, &heads_kv, &ks, &vs, &next_tile};
     const dim3 groups((unsigned)(lay.nk_pad / PAD_GROUP), (unsigned)(p->batch * p->heads_kv));
-    const bool ok = lay.vnat ? hipLaunchKernel(reinterpret_cast<const void*>(&fa_pad_kernel),
-                                               lay.pad ? groups : dim3(1, 1), dim3(256), pad_args,
-                                               0, st) == hipSuccess
-                             : hipLaunchKernel(reinterpret_cast<const void*>(&fa_prep_kernel), groups,
-                                               dim3(256), vt_args, 0, st) == hipSuccess;
+    // The natural-V tile without a key tail needs the pad kernel only for
+    // the counter, which a launch of at most one work item per CU does not
+    // use (fa_pp_body): then nothing runs before the attention kernel.
+    const bool direct = grid_size(p) * splits <= (uint64_t)cus;
+    bool ok = true;
+    if (!lay.vnat)
+      ok = hipLaunchKernel(reinterpret_cast<const void*>(&fa_prep_kernel), groups, dim3(256),
+                           vt_args, 0, st) == hipSuccess;
+    else if (lay.pad || !direct)
+      ok = hipLaunchKernel(reinterpret_cast<const void*>(&fa_pad_kernel),
+                           lay.pad ? groups : dim3(1, 1), dim3(256), pad_args, 0, st) == hipSuccess;
     if (!ok) return FA_ERR_LAUNCH;
   }
 

@@ -242,6 +242,18 @@ def test_kernel_table(lib):
     assert lib.fa_fwd_select(None, C.byref(sel)) == 1
 
 
+def test_automatic_choice_on_invalid_geometry(lib):
+    # The automatic choice looks at query rows per KV head; for a geometry
+    # validation rejects (no KV head, a group that does not divide) it must
+    # not divide by zero: fa_fwd_select still names a tile, and the calls
+    # that validate report the geometry error.
+    sel = C.c_int32()
+    for kw in (dict(heads_kv=0), dict(heads_q=12, heads_kv=5), dict(seq_q=0), dict(heads_q=0)):
+        assert lib.fa_fwd_select(C.byref(problem(**kw)), C.byref(sel)) == 0, kw
+        assert lib.fa_kernel_name(sel.value) == b"pp_n128_r2", kw
+        assert ws_bytes(lib, problem(**kw))[0] == 2, kw
+
+
 def test_automatic_choice(lib):
     # kernel = 0: the 128-key tile for both accumulators, reading V^T with
     # more than 2048 query rows per KV head (group x Nq) and V in its

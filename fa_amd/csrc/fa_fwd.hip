@@ -295,7 +295,9 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, int bytes) {
 // LDS still in flight (vmcnt(0)), which would stall each MFMA step on the
 // loads meant for later blocks. The attention body orders its loads and
 // operand reads itself (explicit vmcnt waits before the barriers that
-// publish a block), and nothing else in these kernels uses M0.
+// publish a block), and nothing else in these kernels uses M0. (M0 is a
+// reserved register to the compiler: naming it as clobbered here only draws
+// a warning per instantiation and yields the same code.)
 __device__ __forceinline__ void dma_to_lds(i32x4 rsrc, uint32_t lds_addr, int voff, int soff) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :: "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff) : "memory");

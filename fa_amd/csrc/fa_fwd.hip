@@ -173,6 +173,20 @@ __device__ __forceinline__ float half_sum(float x) {
   return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
+// acc + the FP16 value in half HI (0 = low, 1 = high) of x, one rounding:
+// v_fma_mix_f32 with the FP16 operand converted exactly and multiplied by
+// 1.0. It runs on the plain VALU pipe; the FP16 dot product v_dot2c_f32_f16
+// (one instruction per pair) measured 3-4 % slower as the softmax's row sum,
+// beside the matrix products of the other wave on the SIMD.
+template <int HI>
+__device__ __forceinline__ float add_f16(float acc, h2 x) {
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(x));
+  else
+    asm("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(x));
+  return acc;
+}
+
 __device__ __forceinline__ f32x16 mfma32(h8 a, h8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
@@ -295,13 +309,17 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, int bytes) {
 // LDS still in flight (vmcnt(0)), which would stall each MFMA step on the
 // loads meant for later blocks. The attention body orders its loads and
 // operand reads itself (explicit vmcnt waits before the barriers that
-// publish a block), and nothing else in these kernels uses M0. (M0 is a
-// reserved register to the compiler: naming it as clobbered here only draws
-// a warning per instantiation and yields the same code.)
+// publish a block). M0 is declared clobbered, so code the compiler places
+// after the load never assumes M0 still holds a value it set earlier; M0 is
+// a reserved register to the compiler, which warns about naming it, and the
+// pragma silences that warning for this function alone.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma_to_lds(i32x4 rsrc, uint32_t lds_addr, int voff, int soff) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :: "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff) : "memory");
+               :: "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // Workgroup barrier that also drains this wave's outstanding LDS operations,
 // so LDS writes issued before it are visible to every wave after it. The
@@ -829,7 +847,6 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
   };
 #pragma unroll
   for (int i = 0; i < KS; ++i) p[i] = h8{};
-  const h2 ones = {(_Float16)1.f, (_Float16)1.f};
 
   // Per-lane operand offsets. QK op (t, kk) reads K row 32t + l32, chunk
   // 2kk + hf. PV op (dt, ks) needs, for dim 32dt + l32, the keys 16ks + 4hf
@@ -993,8 +1010,8 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
     }
     const float mc = m * c;
     // Row sum in four independent partial sums of the FP16-rounded P the PV
-    // products use (one dot per pair), so numerator and denominator use
-    // identical weights.
+    // products use, so numerator and denominator use identical weights: one
+    // mixed-precision add per value (add_f16), on the plain VALU pipe.
     float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
@@ -1009,7 +1026,8 @@ __device__ __forceinline__ void fa_pp_tile(const FaArgs& args, const int tile, c
           const h2 pr = {(_Float16)p0, (_Float16)p1};
           frag[e] = pr[0];
           frag[e + 1] = pr[1];
-          ls[e >> 1] = __builtin_amdgcn_fdot2(pr, ones, ls[e >> 1], false);
+          ls[e >> 1] = add_f16<0>(ls[e >> 1], pr);
+          ls[(e >> 1) ^ 2] = add_f16<1>(ls[(e >> 1) ^ 2], pr);
         }
         p[2 * t + g2] = frag;
       }

@@ -15,7 +15,13 @@ current stream after warmup launches:
   read from LDS (mode 4: twice the traffic, a test of LDS bandwidth), or
   with one wave per SIMD and each LDS read feeding two MFMAs, alone (mode
   5) or with the softmax's VALU mix in the same wave (mode 6): the
-  single-wave layout a 64-row-per-wave tile would need. Its trace records give the clock it ran at.
+  single-wave layout a 64-row-per-wave tile would need. Modes 7-12 run the
+  attention kernel's own skeleton -- its registers, its MFMA step and its
+  two-group ping-pong with a barrier per phase -- with the softmax's VALU
+  step left out (7), whole (9; 8 with the row sum by FP16 dot products, as
+  the kernel had it before), or without its exponentials (10), its FP16
+  packing and row sum (11) or its row sum (12): what each part of the
+  softmax costs beside the matrix products. Its trace records give the clock it ran at.
 * ``gemm`` -- torch's FP16 matrix product (hipBLASLt) on large square and
   rectangular shapes, the rate a tuned vendor GEMM reaches.
 
@@ -39,12 +45,24 @@ GEMM_SHAPES = ((8192, 8192, 8192), (8192, 8192, 16384), (16384, 16384, 8192))
 # MFMA loop modes of libfa_ceiling.so and their labels in measure()'s result.
 MODES = ((0, "registers"), (1, "lds_operand"), (2, "lds_operand_softmax_valu"),
          (3, "lds_operand_read_per_two"), (4, "both_operands_lds"),
-         (5, "one_wave_read_per_two"), (6, "one_wave_read_per_two_softmax_valu"))
+         (5, "one_wave_read_per_two"), (6, "one_wave_read_per_two_softmax_valu"),
+         (7, "pingpong_no_softmax"), (8, "pingpong_softmax_dot2_rowsum"),
+         (9, "pingpong_softmax"), (10, "pingpong_softmax_no_exp"),
+         (11, "pingpong_softmax_no_pack_no_rowsum"), (12, "pingpong_softmax_no_rowsum"))
 MODE_TITLES = {0: "operands in registers", 1: "A operand read from LDS",
                2: "A operand from LDS + the softmax's VALU mix",
                3: "one LDS operand read per two MFMAs", 4: "both operands read from LDS",
                5: "one wave per SIMD, one LDS read per two MFMAs",
-               6: "one wave per SIMD, one LDS read per two MFMAs + the VALU mix in-wave"}
+               6: "one wave per SIMD, one LDS read per two MFMAs + the VALU mix in-wave",
+               7: "attention skeleton: ping-pong MFMA steps and barriers, no softmax",
+               8: "attention skeleton + softmax, row sum by v_dot2c_f32_f16",
+               9: "attention skeleton + softmax as the kernel runs it (row sum by v_fma_mix_f32)",
+               10: "attention skeleton + softmax without the exponentials",
+               11: "attention skeleton + softmax without FP16 packing and row sum",
+               12: "attention skeleton + softmax without the row sum"}
+# Loop iterations per workgroup: 16 MFMAs per wave and iteration in modes
+# 0-6, one 64-MFMA step (two phases) in the ping-pong modes.
+ITERS = {m: (2048 if m >= 7 else 16384) for m, _ in MODES}
 
 
 def _library():
@@ -63,10 +81,12 @@ def _library():
     return lib
 
 
-def mfma_loop(mode, workgroups=2048, iters=16384, reps=3, warmup=2):
+def mfma_loop(mode, workgroups=2048, iters=None, reps=3, warmup=2):
     """(TFLOP/s, trace records) of the MFMA-only kernel in ``mode``."""
     import torch
 
+    if iters is None:
+        iters = ITERS[mode]
     lib = _library()
     g = torch.Generator().manual_seed(7)
     operands = torch.randn(8192, generator=g).half().cuda()
@@ -125,20 +145,29 @@ def gemm(shapes=GEMM_SHAPES, reps=20, warmup=3):
     return rates
 
 
-def measure(gemm_reps=20, loop_iters=16384):
+# The loops bench.py measures beside the forward: the MFMA-only loops and
+# the attention skeleton with its whole softmax step.
+BENCH_MODES = (0, 1, 2, 3, 7, 9)
+
+
+def measure(gemm_reps=20, modes=BENCH_MODES):
     from fa_amd.measure import clock
 
     out = {"gemm_tflops": {}, "mfma_loop": {}}
     for shape, rate in gemm(reps=gemm_reps).items():
         out["gemm_tflops"]["x".join(map(str, shape))] = round(rate, 1)
     for mode, label in MODES:
-        rate, records = mfma_loop(mode, iters=loop_iters)
+        if mode not in modes:
+            continue
+        rate, records = mfma_loop(mode)
         s = clock.summarize(records)
         out["mfma_loop"][label] = {"tflops": round(rate, 1),
                                    "clock_mhz": round(s["mean_mhz_time_weighted"], 0)}
     out["gemm_best_tflops"] = max(out["gemm_tflops"].values())
     out["mfma_loop_best_tflops"] = max(v["tflops"] for v in out["mfma_loop"].values())
     out["softmax_mix_loop_tflops"] = out["mfma_loop"]["lds_operand_softmax_valu"]["tflops"]
+    if "pingpong_softmax" in out["mfma_loop"]:
+        out["skeleton_tflops"] = out["mfma_loop"]["pingpong_softmax"]["tflops"]
     return out
 
 

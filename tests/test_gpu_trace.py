@@ -70,8 +70,8 @@ def test_ceiling_kernel_runs_and_reports_a_clock():
     lib = ceiling._library()
     # Host-side rejections (nothing is launched): unknown mode, no
     # workgroups, misaligned operands.
-    assert lib.fa_ceiling_mfma(7, 1, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
-    assert lib.fa_ceiling_threads(7) == 0 and lib.fa_ceiling_threads(6) == 256
+    assert lib.fa_ceiling_mfma(13, 1, 1, C.c_void_p(16), C.c_void_p(16), None, None) == 1
+    assert lib.fa_ceiling_threads(13) == 0 and lib.fa_ceiling_threads(6) == 256
     assert lib.fa_ceiling_threads(0) == 512
     assert lib.fa_ceiling_flops(0, 3) == lib.fa_ceiling_flops_per_workgroup(3)
     assert lib.fa_ceiling_flops(5, 3) * 2 == lib.fa_ceiling_flops_per_workgroup(3)
@@ -84,4 +84,5 @@ def test_ceiling_kernel_runs_and_reports_a_clock():
         say(f"  mode {mode}: {rate:.1f} TFLOP/s at {s['median_mhz']:.0f} MHz")
         assert 10 < rate < 2600
         assert 100 < s["median_mhz"] < 3000
-        assert np.all(records[:, 6] == 256) and np.all(records[:, 7] == 16)
+        assert np.all(records[:, 6] == 256)
+        assert np.all(records[:, 7] == (64 if mode >= 7 else 16))

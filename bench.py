@@ -12,7 +12,9 @@ Reported, mirroring the reference's metric (``README.md:86-88``: QK/PV FLOPs
 peak): ``value`` = QK/PV TFLOP/s, ``ms_per_step`` = forward milliseconds,
 ``roofline`` against MI355X's dense FP16 MFMA peak (``traffic`` = HBM bytes
 per attention launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-summary for the same workload and tile, null when there is none), and
+summary for the same workload and tile, null when there is none; it is not
+measured in this run, and ``traffic_source`` names the summary file and the
+session it records), and
 ``cpu_baseline`` = the canonical FP32 formula (the oracle's CPU
 restatement) timed on every host core over the full c0 forward, the
 CPU-runnable plumbing configuration (a reported baseline only).
@@ -24,8 +26,9 @@ pairs the mask leaves, 4*B*Hq*D*pairs.
 ``clock`` (HIP backends) is the shader clock the attention kernel ran at,
 from one trace-mode forward after the timed region, with the MFMA roof at
 that clock; ``sustained`` is the board's sustained dense FP16 matrix rate
-measured in the same process (torch FP16 GEMMs, an MFMA-only loop and the
-same loop with LDS operands and the softmax's VALU mix,
+measured in the same process (torch FP16 GEMMs, an MFMA-only loop, the
+same loop with LDS operands and the softmax's VALU mix, and the attention
+kernel's ping-pong skeleton with its softmax step but no data to stage,
 ``fa_amd.measure.ceiling``), with ``value`` as a fraction of each.
 
 ``--copy-mib M`` additionally runs ``--copy-reps`` plain device-to-device
@@ -72,16 +75,19 @@ def parse_args(argv=None):
     return p.parse_args(argv)
 
 
-def traffic_from_profiles(workload_key):
-    """HBM bytes per launch recorded in profiles/*_traffic.txt for this key, or None.
+def traffic_record(workload_key):
+    """(bytes, source) of the HBM traffic per launch committed for this key, or (None, None).
 
-    The summaries hold a line ``key: <workload_key>`` and a line
-    ``traffic_bytes_per_launch: <int>`` (FETCH_SIZE + WRITE_SIZE, each scaled
-    by the copy-kernel calibration factor recorded beside it).
+    The summaries ``profiles/*_traffic.txt`` hold a line ``key:
+    <workload_key>``, a line ``traffic_bytes_per_launch: <int>`` (FETCH_SIZE +
+    WRITE_SIZE, each scaled by the copy-kernel calibration factor recorded
+    beside it) and optionally ``session: <text>`` naming the profiling run;
+    ``source`` names the file and that session, since the value comes from a
+    separate counter run and not from the timed region.
     """
     folder = os.path.join(REPO, "profiles")
     if not os.path.isdir(folder):
-        return None
+        return None, None
     for name in sorted(os.listdir(folder)):
         if not name.endswith("_traffic.txt"):
             continue
@@ -90,10 +96,19 @@ def traffic_from_profiles(workload_key):
             for line in f:
                 key, sep, val = line.partition(":")
                 if sep:
-                    fields[key.strip()] = val.strip()
+                    fields.setdefault(key.strip(), val.strip())
         if fields.get("key") == workload_key and "traffic_bytes_per_launch" in fields:
-            return int(fields["traffic_bytes_per_launch"])
-    return None
+            source = (f"profiles/{name}: rocprofv3 FETCH_SIZE and WRITE_SIZE passes of a "
+                      f"separate profiling run, not measured in this run")
+            if fields.get("session"):
+                source += f" ({fields['session']})"
+            return int(fields["traffic_bytes_per_launch"]), source
+    return None, None
+
+
+def traffic_from_profiles(workload_key):
+    """HBM bytes per launch recorded in profiles/*_traffic.txt for this key, or None."""
+    return traffic_record(workload_key)[0]
 
 
 def cpu_baseline(min_runs=5, budget_s=12.0):
@@ -229,10 +244,13 @@ def main(argv=None):
         sustained["frac_of_mfma_loop"] = round(tflops / sustained["mfma_loop_best_tflops"], 4)
         sustained["frac_of_softmax_mix_loop"] = round(
             tflops / sustained["softmax_mix_loop_tflops"], 4)
+        if "skeleton_tflops" in sustained:
+            sustained["frac_of_skeleton"] = round(tflops / sustained["skeleton_tflops"], 4)
 
     workload_key = f"{args.backend} c{args.case} {case.name} tile={tile_name}"
     if args.causal != "none":
         workload_key += f" causal={args.causal}"
+    traffic, traffic_source = traffic_record(workload_key)
     mask = "non-causal" if args.causal == "none" else f"causal ({args.causal})"
     line = {
         "metric": "fwd ms & QK/PV TFLOPS (% FP16 MFMA peak), B=2 N=131072 Hq=12 D=128",
@@ -264,7 +282,8 @@ def main(argv=None):
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
-            "traffic": traffic_from_profiles(workload_key),
+            "traffic": traffic,
+            "traffic_source": traffic_source,
         },
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(budget_s=args.cpu_seconds),
         "clock": clock_line,

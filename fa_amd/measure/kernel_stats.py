@@ -6,9 +6,11 @@ view ``kernels`` with ``name`` and ``duration`` in ns) or, for runs made with
 kernel: calls, average/min/max duration in ns and share of the total. The
 text is what ``profiles/`` keeps for a workload.
 
-Usage: python -m fa_amd.measure.kernel_stats <rocprofv3 output dir> [--flops F --match NAME]
+Usage: python -m fa_amd.measure.kernel_stats <rocprofv3 output dir> [--flops F --match NAME] [--skip N]
 ``--flops`` adds the achieved TFLOP/s of the kernel whose name contains
-``--match`` (average duration).
+``--match`` (average duration). ``--skip N`` drops the first N dispatches of
+every kernel (in launch order), so that a profile of ``bench.py`` averages its
+timed steps only, not its warmup steps.
 """
 
 import argparse
@@ -20,9 +22,12 @@ import statistics
 
 
 def from_db(path):
+    """{kernel name: [duration ns, ...]} in launch order (by start time when recorded)."""
     con = sqlite3.connect(path)
     try:
-        rows = con.execute("SELECT name, duration FROM kernels").fetchall()
+        cols = {row[1] for row in con.execute("PRAGMA table_info(kernels)")}
+        order = "start" if "start" in cols else "rowid"
+        rows = con.execute(f"SELECT name, duration FROM kernels ORDER BY {order}").fetchall()
     finally:
         con.close()
     out = {}
@@ -40,15 +45,26 @@ def collect(folder):
                 merged.setdefault(k, []).extend(v)
         return merged
     traces = glob.glob(os.path.join(folder, "**", "*_kernel_trace.csv"), recursive=True)
-    merged = {}
+    timed = {}
     for path in traces:
         with open(path, newline="", encoding="utf-8") as f:
             for row in csv.DictReader(f):
-                dur = float(row["End_Timestamp"]) - float(row["Start_Timestamp"])
-                merged.setdefault(row["Kernel_Name"], []).append(dur)
-    if not merged:
+                start, end = float(row["Start_Timestamp"]), float(row["End_Timestamp"])
+                timed.setdefault(row["Kernel_Name"], []).append((start, end - start))
+    if not timed:
         raise FileNotFoundError(f"no rocprofv3 kernel trace under {folder}")
-    return merged
+    return {name: [d for _, d in sorted(v)] for name, v in timed.items()}
+
+
+def skip_first(stats, n):
+    """``stats`` without the first ``n`` dispatches of every kernel (launch order).
+
+    A kernel with no more than ``n`` dispatches keeps its last one, so every
+    kernel of the run still has a line.
+    """
+    if n <= 0:
+        return dict(stats)
+    return {name: (durs[n:] if len(durs) > n else durs[-1:]) for name, durs in stats.items()}
 
 
 def short(name, width=72):
@@ -75,8 +91,10 @@ def main(argv=None):
     p.add_argument("folder")
     p.add_argument("--flops", type=float, default=None)
     p.add_argument("--match", default=None)
+    p.add_argument("--skip", type=int, default=0,
+                   help="drop the first N dispatches of every kernel (warmup steps)")
     args = p.parse_args(argv)
-    print(render(collect(args.folder), args.flops, args.match))
+    print(render(skip_first(collect(args.folder), args.skip), args.flops, args.match))
     return 0
 
 

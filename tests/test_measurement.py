@@ -67,6 +67,35 @@ def test_kernel_stats_from_rocpd_db(tmp_path):
     assert text.splitlines()[1].startswith("hip_fa_fp32acc_kernel")
 
 
+def test_kernel_stats_skips_warmup_dispatches(tmp_path):
+    # A CSV kernel trace written out of launch order: the warmup dispatch
+    # (earliest start, slowest) is the one --skip 1 drops.
+    folder = tmp_path / "csv"
+    folder.mkdir()
+    with open(folder / "run_kernel_trace.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writerow(["attn", 300, 400])     # timed step 2: 100 ns
+        w.writerow(["attn", 0, 180])       # warmup: 180 ns
+        w.writerow(["prep", 290, 300])
+        w.writerow(["attn", 200, 290])     # timed step 1: 90 ns
+    stats = kernel_stats.collect(str(folder))
+    assert stats["attn"] == [180.0, 90.0, 100.0]
+    kept = kernel_stats.skip_first(stats, 1)
+    assert kept["attn"] == [90.0, 100.0]
+    assert kept["prep"] == [10.0]          # a single dispatch is kept
+    assert kernel_stats.skip_first(stats, 0) == stats
+    # The rocpd database is read in start order when it records one.
+    db = tmp_path / "db" / "run_results.db"
+    db.parent.mkdir()
+    con = sqlite3.connect(db)
+    con.execute("CREATE TABLE kernels (name TEXT, start INTEGER, duration INTEGER)")
+    con.executemany("INSERT INTO kernels VALUES (?, ?, ?)", [("k", 50, 7), ("k", 10, 9)])
+    con.commit()
+    con.close()
+    assert kernel_stats.collect(str(tmp_path / "db")) == {"k": [9.0, 7.0]}
+
+
 def test_bench_reads_the_committed_traffic_summary():
     import bench
 
@@ -77,6 +106,11 @@ def test_bench_reads_the_committed_traffic_summary():
     value = bench.traffic_from_profiles(key)
     assert isinstance(value, int) and value > 1_677_721_600   # at least the algorithmic bytes
     assert bench.traffic_from_profiles(key + "x") is None
+    # The JSON line says where the number comes from: not the timed run.
+    value2, source = bench.traffic_record(key)
+    assert value2 == value and source.startswith("profiles/hip_fa_fp32acc_c3_traffic.txt")
+    assert "not measured in this run" in source
+    assert bench.traffic_record(key + "x") == (None, None)
 
 
 def test_counter_summary(tmp_path):
@@ -180,13 +214,16 @@ def test_ceiling_library_host_side():
     per_mfma = 32 * 32 * 16 * 2
     for mode, _ in ceiling.MODES:
         threads = 256 if mode in (5, 6) else 512
+        mfmas = 64 if mode >= 7 else 16     # per wave and iteration
         assert lib.fa_ceiling_threads(mode) == threads
-        assert lib.fa_ceiling_flops(mode, 5) == threads // 64 * 5 * 16 * per_mfma
-        assert mode in ceiling.MODE_TITLES
-    assert [m for m, _ in ceiling.MODES] == list(range(7))
-    assert lib.fa_ceiling_threads(7) == 0 and lib.fa_ceiling_threads(-1) == 0
+        assert lib.fa_ceiling_flops(mode, 5) == threads // 64 * 5 * mfmas * per_mfma
+        assert mode in ceiling.MODE_TITLES and ceiling.ITERS[mode] > 0
+    assert [m for m, _ in ceiling.MODES] == list(range(13))
+    assert set(ceiling.BENCH_MODES) <= {m for m, _ in ceiling.MODES}
+    assert lib.fa_ceiling_threads(13) == 0 and lib.fa_ceiling_threads(-1) == 0
+    assert lib.fa_ceiling_flops(13, 5) == 0
     assert lib.fa_ceiling_flops_per_workgroup(5) == lib.fa_ceiling_flops(0, 5)
-    for bad in ((7, 1, 1, 16, 16), (-1, 1, 1, 16, 16), (0, 0, 1, 16, 16), (0, 1, 0, 16, 16),
+    for bad in ((13, 1, 1, 16, 16), (-1, 1, 1, 16, 16), (0, 0, 1, 16, 16), (0, 1, 0, 16, 16),
                 (0, 1, 1, 24, 16), (0, 1, 1, 16, 8)):
         mode, wg, iters, ops, out = bad
         assert lib.fa_ceiling_mfma(mode, wg, iters, C.c_void_p(ops), C.c_void_p(out), None,

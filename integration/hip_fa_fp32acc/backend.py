@@ -1,8 +1,8 @@
-"""hip_fa -- the MI355X flash-attention forward as a platelett/fa backend.
+"""hip_fa_fp32acc -- the MI355X flash-attention forward as a platelett/fa backend.
 
 Drop-in backend module for the reference harness: copy this directory to
-``backends/hip_fa/`` of platelett/fa and point ``FA_HIP_LIBRARY`` at a built
-``libfa_hip.so`` (or place the library beside this file). It is an
+``backends/hip_fa_fp32acc/`` of platelett/fa and point ``FA_HIP_LIBRARY`` at a
+built ``libfa_hip.so`` (or place the library beside this file). It is an
 ``external`` backend (``core/drivers/external.py:23-26`` of the reference
 drives it unchanged): ``adapt`` sizes the workspace through
 ``fa_fwd_workspace_bytes`` and allocates the output and workspace once per
@@ -11,11 +11,18 @@ same output tensor every time, as the reference's own operator bindings do
 (``backends/cce_fa_nk_nz_vector_fp32_v5_sumpack/binding.py:34-85``). Geometry
 errors raise ``ValueError``, a failed launch ``RuntimeError``.
 
+This module is the FP32-accumulated variant (the reference's FP32-O backend,
+``backends/cce_fa_nk_nz_vector_fp32_v5_sumpack``). Its FP16-accumulated
+sibling ``backends/hip_fa_fp16acc/`` (the reference's FP16-O backend,
+``backends/cce_fa_nqkq_nz_resident_v13_q768_pool_i4_p128``) reuses the library
+loader and the three hooks below with ``acc=1``.
+
 The library's C ABI is declared in ``include/fa_hip.h`` of fa_amd; only three
 of its entry points are needed here. Its device kernels are named
-``hip_fa_fp32acc_kernel<...>`` / ``hip_fa_fp16acc_kernel<...>``, so the
-reference profiler attributes them to this backend by the directory name
-(``core/profiler.py:14-25``).
+``hip_fa_fp32acc_kernel<...>`` / ``hip_fa_fp16acc_kernel<...>``: each contains
+its own backend's directory name and not the other's, so the reference
+profiler's name rule (``core/profiler.py:14-25``) attributes every attention
+kernel to the backend that launched it.
 """
 
 import ctypes as C
@@ -24,7 +31,7 @@ import os
 from core.contract import Meta
 
 META = Meta(
-    name="hip_fa",
+    name="hip_fa_fp32acc",
     type="external",
     op_type="hip_fa_fp32acc_kernel",
     author="fa_amd",
@@ -32,8 +39,8 @@ META = Meta(
           "FP16 MFMA QK/PV, FP32 online softmax, FP32-accumulated O.",
 )
 
-# Accumulation variant (enum fa_acc): 0 = FP32-accumulated O (the headline
-# variant), 1 = FP16-accumulated O.
+# Accumulation variant (enum fa_acc): 0 = FP32-accumulated O (this backend),
+# 1 = FP16-accumulated O (backends/hip_fa_fp16acc).
 ACC = 0
 
 LIBRARY_ENV = "FA_HIP_LIBRARY"
@@ -83,11 +90,11 @@ def _message(status):
     return text.decode() if text else "unknown status"
 
 
-def problem(case, q, k):
+def problem(case, q, k, acc=ACC):
     """The ``fa_problem`` of one forward over canonical q [B,Hq,N,128], k [B,Hkv,N,128]."""
     return FaProblem(batch=q.shape[0], heads_q=q.shape[1], heads_kv=k.shape[1],
                      seq_q=q.shape[2], seq_k=k.shape[2], dim=q.shape[3],
-                     scale=case.scale, acc=ACC, kernel=0, causal=0)
+                     scale=case.scale, acc=acc, kernel=0, causal=0)
 
 
 def build(case):
@@ -97,7 +104,7 @@ def build(case):
                                 f"(set {LIBRARY_ENV})")
 
 
-def adapt(case, canonical):
+def adapt(case, canonical, acc=ACC):
     import torch
 
     q, k, v = canonical["q"], canonical["k"], canonical["v"]
@@ -108,7 +115,7 @@ def adapt(case, canonical):
     if k.shape != v.shape or k.shape[0] != q.shape[0] or q.shape[3] != 128 \
             or k.shape[3] != 128 or q.shape[1] % k.shape[1]:
         raise ValueError("invalid attention geometry for hip_fa")
-    p = problem(case, q, k)
+    p = problem(case, q, k, acc)
     size = C.c_uint64()
     status = _library().fa_fwd_workspace_bytes(C.byref(p), C.byref(size))
     if status:

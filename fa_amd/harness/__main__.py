@@ -8,6 +8,12 @@
                                that has one, on the CPU
   report --cases C,... [--backends B,...] [--iters N] [--out report.csv]
                                timing + check table per configuration
+  kernels <rocprofv3 dir> [--backends B,...] [--skip N]
+                               each backend's mean device-kernel duration in a
+                               ``rocprofv3 --kernel-trace`` run (for example of
+                               ``report``), attributed by the reference
+                               profiler's kernel-name rule; kernels no backend
+                               owns (the HIP prep kernel) are listed apart
 
 Configurations are named ``c0``..``c4`` (this repository's table, which
 begins with the CPU-sized c0) or by their full case name
@@ -63,6 +69,11 @@ def main(argv=None) -> int:
     p_rep.add_argument("--iters", type=int, default=20)
     p_rep.add_argument("--no-check", action="store_true")
     p_rep.add_argument("--out")
+    p_ker = sub.add_parser("kernels")
+    p_ker.add_argument("trace_dir")
+    p_ker.add_argument("--backends")
+    p_ker.add_argument("--skip", type=int, default=0,
+                       help="drop the first N dispatches of every kernel (warmup calls)")
     for p in (p_check, p_rep):
         p.add_argument("--seed", type=int, default=0)
         p.add_argument("--atol", type=float, default=1e-2)
@@ -90,6 +101,15 @@ def main(argv=None) -> int:
         for n in names:
             built = catalog.build(n, CASES[0])
             print(f"BUILD {n} {'done' if built else 'nothing to build'}")
+        return 0
+
+    if args.command == "kernels":
+        from fa_amd.harness.timing import KernelOwners, kernel_table, render_kernel_table
+
+        names = args.backends.split(",") if args.backends else catalog.names()
+        owners = KernelOwners(names, op_types={n: catalog[n].meta.op_type for n in names})
+        table, unowned = kernel_table(args.trace_dir, owners, skip=args.skip)
+        print(render_kernel_table(table, unowned))
         return 0
 
     tol = report.Tolerance(args.atol, args.rtol)

@@ -8,13 +8,17 @@ The reference reads the same quantity from its NPU profiler's kernel table
 (3 warmup and 20 timed calls, ``core/profiler.py:28-85`` there).
 
 ``KernelOwners`` attributes kernel names from a ``rocprofv3 --kernel-trace``
-CSV to backends, by the identity rule of the reference's plugin API
+run to backends, by the identity rule of the reference's plugin API
 (``core/profiler.py:14-25``): a backend that declares its exact device
 symbol owns only that symbol (and never claims a kernel by substring);
 every other backend owns the kernels whose name contains its directory name
 or its ``META.op_type``. A backend's exact symbol defaults to
 ``<directory>_kernel``. Explicit symbols are tried before any substring, so
 ``abc_kernel`` cannot be claimed by a backend called ``ab``.
+``kernel_table`` applies it to a whole trace: each backend's mean device
+kernel duration, the quantity the reference's profiler reports per backend
+(``core/profiler.py:28-85``), with kernels no backend owns (for the HIP
+backends, the prep kernel) listed apart.
 """
 
 from __future__ import annotations
@@ -72,3 +76,43 @@ class KernelOwners:
                     durations[b].append(ns / 1e3)
         return {b: (sum(durations[b]) / len(durations[b]) if durations[b] else None)
                 for b in self.backends}
+
+
+def kernel_table(trace_dir, owners: KernelOwners, skip: int = 0):
+    """Per-backend kernel durations of a rocprofv3 kernel trace.
+
+    Reads every dispatch under ``trace_dir`` (CSV or rocpd output, via
+    ``fa_amd.measure.kernel_stats``), drops the first ``skip`` dispatches of
+    every kernel (warmup calls), and returns ``(per_backend, unowned)``:
+    ``per_backend[b] = {"dispatches": n, "mean_us": ..., "kernels": [names]}``
+    (None for a backend with no dispatch) and ``unowned[name] = (n, mean_us)``.
+    """
+    from fa_amd.measure import kernel_stats
+
+    stats = kernel_stats.skip_first(kernel_stats.collect(trace_dir), skip)
+    per = {b: [] for b in owners.backends}
+    names = {b: [] for b in owners.backends}
+    unowned = {}
+    for name, durs in stats.items():
+        b = owners.owner(name)
+        if b is None:
+            unowned[name] = (len(durs), sum(durs) / len(durs) / 1e3)
+        else:
+            per[b].extend(durs)
+            names[b].append(name)
+    table = {b: ({"dispatches": len(d), "mean_us": sum(d) / len(d) / 1e3, "kernels": names[b]}
+                 if d else None) for b, d in per.items()}
+    return table, unowned
+
+
+def render_kernel_table(table, unowned):
+    lines = [f"{'Backend':<18} {'Dispatches':>10} {'Kernel_us':>14}  Kernels"]
+    for b, row in table.items():
+        if row is None:
+            lines.append(f"{b:<18} {0:>10} {'N/A':>14}  (no kernel of this backend in the trace)")
+        else:
+            lines.append(f"{b:<18} {row['dispatches']:>10} {row['mean_us']:>14,.2f}  "
+                         + "; ".join(row["kernels"]))
+    for name, (n, us) in sorted(unowned.items(), key=lambda kv: -kv[1][0] * kv[1][1]):
+        lines.append(f"{'(unowned)':<18} {n:>10} {us:>14,.2f}  {name}")
+    return "\n".join(lines)

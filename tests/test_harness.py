@@ -298,6 +298,41 @@ def test_hip_kernels_are_attributed_to_their_backend(tmp_path):
                                         "torch_ref": None}
 
 
+def test_kernels_command_reports_per_backend_kernel_time(tmp_path, capsys):
+    """``python -m fa_amd.harness kernels <dir>``: each backend's mean kernel
+    duration from a rocprofv3 CSV trace (warmup dispatches skipped), the prep
+    kernel listed as unowned."""
+    from fa_amd.harness.__main__ import main
+
+    k32 = "_ZN12_GLOBAL__N_121hip_fa_fp32acc_kernelILi128ELi2ELi0ELb0ELb0EEEvNS_6FaArgsE"
+    k16 = k32.replace("fp32acc", "fp16acc")
+    prep = "_ZN12_GLOBAL__N_114fa_prep_kernelEPKDF16_"
+    folder = tmp_path / "run"
+    folder.mkdir()
+    rows = [(k32, 0, 9000), (prep, 9000, 9100), (k32, 10000, 12000), (k32, 20000, 24000),
+            (k16, 30000, 39000), (k16, 40000, 45000), (prep, 45000, 45300)]
+    with open(folder / "run_kernel_trace.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writerows(rows)
+    cat = Catalog.default()
+    names = ["hip_fa_fp32acc", "hip_fa_fp16acc", "torch_ref"]
+    owners = timing.KernelOwners(names, op_types={n: cat[n].meta.op_type for n in names})
+    table, unowned = timing.kernel_table(str(folder), owners, skip=1)
+    assert table["hip_fa_fp32acc"]["dispatches"] == 2
+    assert table["hip_fa_fp32acc"]["mean_us"] == pytest.approx(3.0)      # (2 + 4) / 2 us
+    assert table["hip_fa_fp16acc"]["mean_us"] == pytest.approx(5.0)
+    assert table["torch_ref"] is None
+    assert unowned == {prep: (1, pytest.approx(0.3))}
+    assert main(["kernels", str(folder), "--backends", ",".join(names), "--skip", "1"]) == 0
+    out = capsys.readouterr().out.splitlines()
+    assert out[0].split()[:3] == ["Backend", "Dispatches", "Kernel_us"]
+    assert out[1].split()[:3] == ["hip_fa_fp32acc", "2", "3.00"]
+    assert out[2].split()[:3] == ["hip_fa_fp16acc", "1", "5.00"]
+    assert out[3].startswith("torch_ref") and "N/A" in out[3]
+    assert out[4].startswith("(unowned)") and prep in out[4]
+
+
 # --------------------------------------------------------------------------- CLI
 
 def test_cli_names_configurations_by_c_index_or_case_name():

@@ -283,6 +283,12 @@ const char* fa_kernel_name(int32_t kernel);
  * array and each call overwrites what it uses, so calls that overlap on one
  * GPU (different streams, or threads) race and must be serialised by the
  * caller; the array's contents on entry do not matter.
+ * Graph capture: the first call of a problem's tile and variant on a device
+ * also does host-side set-up (the scratch address, the kernel's dynamic-LDS
+ * limit, the CU count), which is not a stream operation; make that first
+ * call outside any capture. After it, a call issues kernel launches only
+ * (no memset, no allocation) and can be captured in a HIP graph; replays
+ * read the inputs in place (GPU-tested).
  */
 #define FA_NOALLOC_SCRATCH_BYTES ((64ull << 20) + (64ull << 10))
 int fa_fwd_noalloc(const fa_problem* p, const void* q, const void* k, const void* v, void* o,

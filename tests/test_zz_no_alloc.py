@@ -5,7 +5,8 @@ per GPU). Called through the C ABI, it must give exactly fa_fwd's output (the
 same kernels, only the workspace differs), on two calls in a row, the second
 with a smaller input (ragged ones, which also use the padded copies in the
 scratch, through both V layouts), and refuse problems whose workspace exceeds the array before any
-work is enqueued.
+work is enqueued. Captured in a HIP graph after a first eager call, its
+replays must equal fa_fwd on the same inputs.
 """
 
 import ctypes as C
@@ -77,6 +78,39 @@ def test_noalloc_headline_size_fits_and_oversize_is_refused(library_path):
     assert lib.fa_fwd_workspace_bytes(C.byref(c3), C.byref(size)) == 0
     assert size.value <= binding.NOALLOC_SCRATCH_BYTES
     big = binding.FaProblem(4, 12, 1, 256, 131071, 128, 128 ** -0.5, 0, 0, 0)   # ragged: 256 MiB
-    fake = C.c_void_p(4096)
-    assert lib.fa_fwd_noalloc(C.byref(big), fake, fake, fake, fake, None) == 14
+    # No tensors: the size check comes before the null check, so the refusal
+    # is FA_ERR_SCRATCH, and a regression would return FA_ERR_NULL without
+    # enqueuing anything.
+    assert lib.fa_fwd_noalloc(C.byref(big), None, None, None, None, None) == 14
     assert b"scratch" in lib.fa_strerror(14)
+
+
+def test_noalloc_captured_in_a_graph_replays_like_eager_calls(library_path):
+    """fa_fwd_noalloc captured in a HIP graph (after a first eager call on the
+    device, as the header asks): every replay, with eager work and new input
+    values between replays, equals fa_fwd on the same inputs bit for bit."""
+    lib = binding.load_library(library_path)
+    b, hq, hkv, nq, nk = 1, 12, 1, 1024, 1000          # ragged keys: prep + attention kernels
+    say(f"case noalloc graph: B={b} Hq={hq} Hkv={hkv} Nq={nq} Nk={nk}")
+    prob = binding.FaProblem(b, hq, hkv, nq, nk, 128, 128 ** -0.5, 0, 0, 0)
+    sets = [inputs(b, hq, hkv, nq, nk, seed=s) for s in (21, 22)]
+    want = [with_workspace(lib, prob, *x) for x in sets]
+    q, k, v = (t.clone() for t in sets[0])
+    out = torch.empty_like(q)
+    without_workspace(lib, prob, q, k, v)                # first call: host-side set-up
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.fa_fwd_noalloc(C.byref(prob), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                out.data_ptr(), C.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, lib.fa_strerror(rc)
+    for replay in range(4):
+        src = sets[replay % 2]
+        for dst, t in zip((q, k, v), src):
+            dst.copy_(t)
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        say(f"  replay {replay}")
+        assert torch.equal(out, want[replay % 2]), replay
+    del graph

@@ -8,7 +8,7 @@
                                that has one, on the CPU
   report --cases C,... [--backends B,...] [--iters N] [--out report.csv]
                                timing + check table per configuration
-  kernels <rocprofv3 dir> [--backends B,...] [--skip N]
+  kernels <rocprofv3 dir> [--backends B,...] [--skip N] [--unowned N]
                                each backend's mean device-kernel duration in a
                                ``rocprofv3 --kernel-trace`` run (for example of
                                ``report``), attributed by the reference
@@ -74,6 +74,8 @@ def main(argv=None) -> int:
     p_ker.add_argument("--backends")
     p_ker.add_argument("--skip", type=int, default=0,
                        help="drop the first N dispatches of every kernel (warmup calls)")
+    p_ker.add_argument("--unowned", type=int, default=5,
+                       help="list this many unowned kernels (by device time), then their total")
     for p in (p_check, p_rep):
         p.add_argument("--seed", type=int, default=0)
         p.add_argument("--atol", type=float, default=1e-2)
@@ -109,7 +111,7 @@ def main(argv=None) -> int:
         names = args.backends.split(",") if args.backends else catalog.names()
         owners = KernelOwners(names, op_types={n: catalog[n].meta.op_type for n in names})
         table, unowned = kernel_table(args.trace_dir, owners, skip=args.skip)
-        print(render_kernel_table(table, unowned))
+        print(render_kernel_table(table, unowned, args.unowned))
         return 0
 
     tol = report.Tolerance(args.atol, args.rtol)

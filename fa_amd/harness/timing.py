@@ -105,7 +105,9 @@ def kernel_table(trace_dir, owners: KernelOwners, skip: int = 0):
     return table, unowned
 
 
-def render_kernel_table(table, unowned):
+def render_kernel_table(table, unowned, max_unowned=5):
+    """Text table: one line per backend, then the ``max_unowned`` unowned
+    kernels with the most device time and a line summing the rest."""
     lines = [f"{'Backend':<18} {'Dispatches':>10} {'Kernel_us':>14}  Kernels"]
     for b, row in table.items():
         if row is None:
@@ -113,6 +115,11 @@ def render_kernel_table(table, unowned):
         else:
             lines.append(f"{b:<18} {row['dispatches']:>10} {row['mean_us']:>14,.2f}  "
                          + "; ".join(row["kernels"]))
-    for name, (n, us) in sorted(unowned.items(), key=lambda kv: -kv[1][0] * kv[1][1]):
+    ranked = sorted(unowned.items(), key=lambda kv: -kv[1][0] * kv[1][1])
+    for name, (n, us) in ranked[:max_unowned]:
         lines.append(f"{'(unowned)':<18} {n:>10} {us:>14,.2f}  {name}")
+    rest = ranked[max_unowned:]
+    if rest:
+        lines.append(f"{'(unowned)':<18} {sum(n for _, (n, _) in rest):>10} {'':>14}  "
+                     f"... {len(rest)} more kernels, {sum(n * us for _, (n, us) in rest):,.0f} us in all")
     return "\n".join(lines)

@@ -101,6 +101,8 @@ def main(argv=None):
                    help="configuration index c0..c4 (its Q+K+V+O bytes are the algorithmic bytes)")
     p.add_argument("--command-fetch", default="")
     p.add_argument("--command-write", default="")
+    p.add_argument("--session", default="",
+                   help="which profiling run the passes come from (bench.py names it beside the value)")
     p.add_argument("--out", required=True)
     args = p.parse_args(argv)
     s = summarize(args.fetch, args.write, args.copy_mib)
@@ -111,6 +113,10 @@ def main(argv=None):
     lines = [
         "# HBM traffic per launch (rocprofv3 FETCH_SIZE and WRITE_SIZE, separate passes)",
         f"key: {args.key}",
+    ]
+    if args.session:
+        lines.append(f"session: {args.session}")
+    lines += [
         f"command_fetch: {args.command_fetch}",
         f"command_write: {args.command_write}",
         f"attention_kernel: {s['attention_kernel']}",

@@ -98,8 +98,16 @@ def test_c4_worst_rows_match_the_model(library_path, acc):
     out = op(dev["q"], dev["k"], dev["v"]).clone()
     ref = torch_ref.attention(dev["q"], dev["k"], dev["v"], case.scale)
     torch.cuda.synchronize()
-    row_err = (out.float() - ref.float()).abs().amax(dim=3).cpu().numpy()     # [B, Hq, Nq]
-    del ref
+    diff = (out.float() - ref.float()).abs()
+    row_err = diff.amax(dim=3).cpu().numpy()                                   # [B, Hq, Nq]
+    # The reference harness's own check (core/bench.py:139, atol = rtol = 1e-2),
+    # row by row: the model of the reference kernels' roundings fails it on
+    # about 4 % of c4's rows (tests/test_reference_model.py); this kernel on
+    # at most one row in ten thousand.
+    failing = int((diff > 1e-2 + 1e-2 * ref.float().abs()).any(dim=3).sum())
+    say(f"  rows failing the reference harness's check: {failing} of {row_err.size}")
+    assert failing <= row_err.size // 10000
+    del ref, diff
     worst = np.argsort(row_err.ravel())[-24:]
     shape = row_err.shape
     rows = {tuple(int(x) for x in np.unravel_index(f, shape)) for f in worst}

@@ -1684,6 +1684,17 @@ int device_cus(int* cus) {
   return FA_OK;
 }
 
+// The per-device state above is looked up for the current device, so a
+// launch's stream must be one of that device's (the null stream always is).
+int check_stream_device(void* stream) {
+  if (!stream) return FA_OK;
+  int dev = 0, sdev = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), &sdev) != hipSuccess)
+    return FA_ERR_LAUNCH;
+  return sdev == dev ? FA_OK : FA_ERR_DEVICE;
+}
+
 // Optional outputs of one launch (per-row LSE, capture statistics, trace
 // records) and the synchronous debug mode.
 struct Extras {
@@ -1742,6 +1753,8 @@ int launch(const fa_problem* p, const fa_strides* strides, const void* q, const 
                    : ex.sync  ? MODE_SYNC
                               : MODE_RUN;
   const int packed = row_layout(p).pack > 1 ? 1 : 0;
+  rc = check_stream_device(stream);
+  if (rc) return rc;
   rc = ensure_lds_limit(tile, packed, acc, mode);
   if (rc) return rc;
   if (!cus) {
@@ -2058,6 +2071,7 @@ const char* fa_strerror(int status) {
     case FA_ERR_TRACE: return "trace needs a buffer of fa_fwd_trace_count() 64-bit words";
     case FA_ERR_SCRATCH: return "problem needs more workspace than fa_fwd_noalloc's scratch (FA_NOALLOC_SCRATCH_BYTES)";
     case FA_ERR_SPLIT: return "split count outside 0..1024 (or a negative CU count)";
+    case FA_ERR_DEVICE: return "stream belongs to another device than the current one";
     default: return "unknown status";
   }
 }

@@ -41,7 +41,11 @@
  *     the CU count, and the address of fa_fwd_noalloc()'s static scratch
  *     array (each set on first use);
  *   - fa_fwd() is asynchronous on the given stream (a hipStream_t passed as
- *     void*, NULL for the default stream).
+ *     void*, NULL for the default stream);
+ *   - calls are made with the tensors' device current (hipSetDevice; torch:
+ *     `with torch.cuda.device(...)`), since the per-device state above is
+ *     looked up for the current device: a stream of another device is
+ *     refused with FA_ERR_DEVICE before anything is enqueued.
  *
  * This header needs no HIP or torch headers, so any FFI (ctypes, cgo, JNI)
  * can bind it directly.
@@ -71,7 +75,8 @@ enum fa_status {
   FA_ERR_CAUSAL = 12,       /* unknown causal mode */
   FA_ERR_TRACE = 13,        /* trace buffer too small */
   FA_ERR_SCRATCH = 14,      /* fa_fwd_noalloc: workspace need above FA_NOALLOC_SCRATCH_BYTES */
-  FA_ERR_SPLIT = 15         /* split count outside 0..1024, or a negative CU count */
+  FA_ERR_SPLIT = 15,        /* split count outside 0..1024, or a negative CU count */
+  FA_ERR_DEVICE = 16        /* the stream belongs to another device than the current one */
 };
 
 enum fa_acc {

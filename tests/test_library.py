@@ -222,6 +222,9 @@ def test_fwd_rejects_before_launch(lib):
     # fa_fwd_lse: same checks, plus the lse pointer's alignment (NULL is allowed).
     assert lib.fa_fwd_lse(C.byref(prob), p, p, p, p, odd, p, size, None) == 5
     assert lib.fa_fwd_lse(C.byref(prob), None, p, p, p, None, p, size, None) == 1
+    # A stream must belong to the current device (checked at launch, after the
+    # host-side checks above); the code has its own message.
+    assert b"device" in lib.fa_strerror(16)
 
 
 def test_kernel_table(lib):

@@ -129,10 +129,12 @@ def call(op_args):
     import torch
 
     a = op_args
-    stream = torch.cuda.current_stream(a["q"].device)
-    status = _library().fa_fwd(C.byref(a["problem"]), a["q"].data_ptr(), a["k"].data_ptr(),
-                               a["v"].data_ptr(), a["out"].data_ptr(), a["workspace"].data_ptr(),
-                               a["workspace"].numel(), C.c_void_p(stream.cuda_stream))
+    with torch.cuda.device(a["q"].device):     # the library works on the current device
+        stream = torch.cuda.current_stream(a["q"].device)
+        status = _library().fa_fwd(C.byref(a["problem"]), a["q"].data_ptr(), a["k"].data_ptr(),
+                                   a["v"].data_ptr(), a["out"].data_ptr(),
+                                   a["workspace"].data_ptr(), a["workspace"].numel(),
+                                   C.c_void_p(stream.cuda_stream))
     if status:
         raise RuntimeError(f"fa_fwd launch: {status} ({_message(status)})")
     return a["out"]

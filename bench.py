@@ -31,6 +31,13 @@ same loop with LDS operands and the softmax's VALU mix, and the attention
 kernel's ping-pong skeleton with its softmax step but no data to stage,
 ``fa_amd.measure.ceiling``), with ``value`` as a fraction of each.
 
+``configs`` (HIP backends, full attention) times the configurations
+``--configs`` (default all of c0..c4; ``--configs ""`` for none) with both
+accumulation variants after the headline, in the same process: canonical
+inputs, ``--config-warmup`` untimed and ``--config-steps`` timed forwards
+each, HIP events around the timed ones (the headline's own entry is the
+headline measurement).
+
 ``--copy-mib M`` additionally runs ``--copy-reps`` plain device-to-device
 copies of M MiB after the timed region, untimed: the calibration kernel the
 traffic summary scales the FETCH_SIZE and WRITE_SIZE counters by.
@@ -72,7 +79,63 @@ def parse_args(argv=None):
     p.add_argument("--copy-reps", type=int, default=3)
     p.add_argument("--no-ceiling", action="store_true",
                    help="skip the sustained-rate (GEMM and MFMA loop) and clock measurements")
+    p.add_argument("--configs", default="0,1,2,3,4",
+                   help="configurations to time with both accumulation variants ('' = none)")
+    p.add_argument("--config-steps", type=int, default=5)
+    p.add_argument("--config-warmup", type=int, default=2)
     return p.parse_args(argv)
+
+
+def time_forward(call, steps, warmup):
+    """Milliseconds per call: ``warmup`` untimed calls, then ``steps`` calls
+    between HIP events on torch's current stream (where the kernels run)."""
+    import torch
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        call()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def config_table(indices, steps, warmup, headline=None):
+    """{"c<i>": {"fp32": {...}, "fp16": {...}}} over configurations ``indices``:
+    ms per forward, QK/PV TFLOP/s and percent of the FP16 peak, full
+    attention. ``headline`` = (case index, acc, ms) is entered as measured."""
+    import torch
+
+    from fa_amd.backends import hip_common
+    from fa_amd.problem.canonical import build_canonical
+    from fa_amd.problem.cases import CASES
+
+    table = {}
+    for i in indices:
+        case = CASES[i]
+        x = None
+        row = {}
+        for acc in ("fp32", "fp16"):
+            if headline is not None and headline[:2] == (i, acc):
+                ms = headline[2]
+            else:
+                if x is None:
+                    x = build_canonical(case, 0, device="cuda")
+                op = hip_common.operator(acc, case)
+                ms = time_forward(lambda: op(x["q"], x["k"], x["v"]), steps, warmup)
+                del op
+            tflops = case.flops / (ms * 1e-3) / 1e12
+            row[acc] = {"ms": round(ms, 4), "tflops": round(tflops, 1),
+                        "pct_peak": round(100 * tflops / PEAK_FP16_TFLOPS, 2)}
+        row["workload"] = case.name
+        table[f"c{i}"] = row
+        del x
+        torch.cuda.empty_cache()
+    return table
 
 
 def traffic_record(workload_key):
@@ -194,17 +257,7 @@ def main(argv=None):
             # Explicit tile configuration (tuning runs) or a causal mask.
             call = lambda: op(canonical["q"], canonical["k"], canonical["v"])  # noqa: E731
 
-    for _ in range(args.warmup):
-        call()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(args.steps):
-        call()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    ms = time_forward(call, args.steps, args.warmup)
     flops = (4 * case.batch * case.heads_q * case.dim
              * visible_pairs(case.seq_len, case.seq_len, args.causal))
     tflops = flops / (ms * 1e-3) / 1e12
@@ -247,6 +300,15 @@ def main(argv=None):
         if "skeleton_tflops" in sustained:
             sustained["frac_of_skeleton"] = round(tflops / sustained["skeleton_tflops"], 4)
 
+    configs = None
+    indices = [int(c) for c in args.configs.split(",") if c.strip()]
+    if acc is not None and indices:
+        same = args.causal == "none" and not args.kernel and args.seed == 0
+        headline = (args.case, acc, ms) if same else None
+        del call, bind, canonical
+        torch.cuda.empty_cache()
+        configs = config_table(indices, args.config_steps, args.config_warmup, headline)
+
     workload_key = f"{args.backend} c{args.case} {case.name} tile={tile_name}"
     if args.causal != "none":
         workload_key += f" causal={args.causal}"
@@ -288,6 +350,7 @@ def main(argv=None):
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(budget_s=args.cpu_seconds),
         "clock": clock_line,
         "sustained": sustained,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
     return 0

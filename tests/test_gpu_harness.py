@@ -50,7 +50,8 @@ def test_bench_json_line(causal):
     print(f"case bench.py c0 causal={causal}", flush=True)
     proc = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--case", "0",
                            "--steps", "3", "--warmup", "1", "--cpu-seconds", "1",
-                           "--causal", causal], capture_output=True, text=True, timeout=240)
+                           "--causal", causal, "--configs", "0,1"],
+                          capture_output=True, text=True, timeout=240)
     assert proc.returncode == 0, proc.stderr[-2000:]
     line = json.loads(proc.stdout.strip().splitlines()[-1])
     for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
@@ -64,3 +65,13 @@ def test_bench_json_line(causal):
     cpu = line["cpu_baseline"]
     assert cpu["kind"] == "port" and cpu["value"] > 0 and cpu["cores"] == os.cpu_count()
     assert cpu["sample"].startswith("c0 B1_S4096_Q12_KV1_D128: the full forward")
+    # Both variants of the configurations asked for, full attention; the
+    # headline's own entry is the headline measurement when it is one of them.
+    table = line["configs"]
+    assert sorted(table) == ["c0", "c1"]
+    assert table["c1"]["workload"] == "B1_S32768_Q12_KV1_D128"
+    for row in table.values():
+        for acc in ("fp32", "fp16"):
+            assert row[acc]["ms"] > 0 and row[acc]["tflops"] > 0
+    if causal == "none":
+        assert table["c0"]["fp32"]["ms"] == round(line["ms_per_step"], 4)

@@ -132,6 +132,7 @@ def test_bench_cli_contract():
     args = bench.parse_args([])
     assert (args.gpus, args.case, args.causal, args.kernel) == (1, 3, "none", 0)
     assert bench.parse_args(["--causal", "bottom_right"]).causal == "bottom_right"
+    assert bench.parse_args([]).configs == "0,1,2,3,4"
     # More than one GPU is refused before anything touches a device.
     assert bench.main(["--gpus", "2"]) == 2
 

@@ -1685,12 +1685,13 @@ int device_cus(int* cus) {
 }
 
 // The per-device state above is looked up for the current device, so a
-// launch's stream must be one of that device's (the null stream always is).
+// launch's stream must be one of that device's (the null, legacy and
+// per-thread default streams always are).
 int check_stream_device(void* stream) {
-  if (!stream) return FA_OK;
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!st || st == hipStreamLegacy || st == hipStreamPerThread) return FA_OK;
   int dev = 0, sdev = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), &sdev) != hipSuccess)
+  if (hipGetDevice(&dev) != hipSuccess || hipStreamGetDevice(st, &sdev) != hipSuccess)
     return FA_ERR_LAUNCH;
   return sdev == dev ? FA_OK : FA_ERR_DEVICE;
 }

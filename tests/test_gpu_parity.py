@@ -755,6 +755,36 @@ def test_concurrent_streams_independent(library_path):
         assert bool(torch.equal(out_a, ref_a)) and bool(torch.equal(out_b, ref_b))
 
 
+def test_special_stream_handles(library_path):
+    """The C ABI takes HIP's special stream handles (legacy 1, per-thread 2)
+    as streams of the current device, like the null stream: the same output
+    as a launch on torch's stream."""
+    import ctypes as C
+
+    from fa_amd import binding
+
+    say("case special stream handles")
+    lib = binding.load_library(library_path)
+    g = torch.Generator().manual_seed(23)
+    q = torch.randn(1, 4, 700, 128, generator=g, dtype=torch.float16).cuda()
+    k, v = (torch.randn(1, 2, 900, 128, generator=g, dtype=torch.float16).cuda()
+            for _ in range(2))
+    prob = binding.FaProblem(1, 4, 2, 700, 900, 128, 128 ** -0.5, 0, 0, 0)
+    size = C.c_uint64()
+    assert lib.fa_fwd_workspace_bytes(C.byref(prob), C.byref(size)) == 0
+    ws = torch.empty(max(size.value, 16), dtype=torch.uint8, device="cuda")
+    outs = []
+    for handle in (torch.cuda.current_stream().cuda_stream, 1, 2):
+        out = torch.empty_like(q)
+        torch.cuda.synchronize()
+        rc = lib.fa_fwd(C.byref(prob), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                        ws.data_ptr(), ws.numel(), C.c_void_p(handle))
+        assert rc == 0, lib.fa_strerror(rc)
+        torch.cuda.synchronize()
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
 def test_graph_capture_replays(library_path):
     """fa_fwd captured in a HIP graph: every replay (with eager work and
     synchronisation in between, inputs changed in place) equals the eager

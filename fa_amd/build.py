@@ -7,7 +7,14 @@ Two libraries:
 * ``libfa_ceiling.so`` -- a measurement kernel that issues nothing but FP16
   MFMAs, for the board's sustained matrix rate
   (``fa_amd/csrc/measure/mfma_ceiling.hip``); never loaded by the attention
-  path.
+  path;
+* on request (``--sanitize``), ``libfa_hip_hostsan.so`` -- the attention
+  library with its host code (the C ABI's validation, sizing and launch
+  set-up) built with AddressSanitizer and UndefinedBehaviorSanitizer; the
+  device code is unchanged. Load it with the clang ASan runtime preloaded
+  (``LD_PRELOAD=$(hipcc -print-file-name=libclang_rt.asan-x86_64.so)
+  ASAN_OPTIONS=detect_leaks=0``) and point the tests at it with
+  ``FA_TEST_LIBRARY``.
 
 A library's build identity is the SHA-256 of every source and header it is
 compiled from and of the compiler command line (the hipcc version is recorded
@@ -53,6 +60,7 @@ class Target:
     name: str          # library file name
     hip: tuple         # HIP sources, relative to CSRC
     headers: tuple     # headers the build depends on, relative to REPO
+    flags: tuple = ()  # extra compiler flags of this target
 
     @property
     def library(self) -> Path:
@@ -69,6 +77,14 @@ class Target:
 ATTENTION = Target("libfa_hip.so", ("fa_fwd.hip",), ("include/fa_hip.h",))
 CEILING = Target("libfa_ceiling.so", ("measure/mfma_ceiling.hip",), ())
 TARGETS = (ATTENTION, CEILING)
+# Host-side sanitizers only (each -fsanitize= behind -Xarch_host): GPU code
+# is never built with them.
+HOSTSAN = Target("libfa_hip_hostsan.so", ("fa_fwd.hip",), ("include/fa_hip.h",), (
+    "-g",
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-omit-frame-pointer",
+))
 
 # The attention library (what the product path loads).
 LIBRARY = ATTENTION.library
@@ -92,7 +108,7 @@ def identity(target=ATTENTION):
     for path in target.sources():
         h.update(str(path.relative_to(REPO)).encode())
         h.update(path.read_bytes())
-    h.update(" ".join(FLAGS).encode())
+    h.update(" ".join(FLAGS + target.flags).encode())
     return h.hexdigest()
 
 
@@ -134,7 +150,8 @@ def _compile(target, verbose):
     ident = identity(target)
     with tempfile.TemporaryDirectory(dir=LIBDIR) as tmp:
         out = Path(tmp) / target.name
-        cmd = [HIPCC, *FLAGS, f"-I{INCLUDE}", *(str(CSRC / s) for s in target.hip), "-o", str(out)]
+        cmd = [HIPCC, *FLAGS, *target.flags, f"-I{INCLUDE}", *(str(CSRC / s) for s in target.hip),
+               "-o", str(out)]
         if verbose:
             print(" ".join(cmd))
         res = subprocess.run(cmd, capture_output=True, text=True, cwd=tmp)
@@ -147,7 +164,7 @@ def _compile(target, verbose):
         "identity": ident,
         "sha256": hashlib.sha256(target.library.read_bytes()).hexdigest(),
         "arch": ARCH,
-        "flags": list(FLAGS),
+        "flags": list(FLAGS + target.flags),
         "hipcc": _hipcc_version(),
         "sources": [str(p.relative_to(REPO)) for p in target.sources()],
     }, indent=1))
@@ -159,8 +176,12 @@ def _compile(target, verbose):
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--force", action="store_true", help="rebuild even when up to date")
+    ap.add_argument("--sanitize", action="store_true",
+                    help="also build libfa_hip_hostsan.so (host code under ASan and UBSan)")
     args = ap.parse_args(argv)
     build_all(force=args.force, verbose=True)
+    if args.sanitize:
+        build(force=args.force, verbose=True, target=HOSTSAN)
 
 
 if __name__ == "__main__":

@@ -14,9 +14,14 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def library_path():
-    """Path of the built C-ABI library; builds it (content-hashed) when absent."""
+    """Path of the built C-ABI library; builds it (content-hashed) when absent.
+    ``FA_TEST_LIBRARY`` names another build of it to test instead (e.g. the
+    host-sanitizer build, ``python -m fa_amd.build --sanitize``)."""
     from fa_amd import build
 
+    other = os.environ.get("FA_TEST_LIBRARY")
+    if other:
+        return other
     if not build.up_to_date():
         build.build()
     return str(build.LIBRARY)

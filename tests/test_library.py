@@ -417,3 +417,18 @@ def test_split_rejects_before_launch(lib):
                     {"splits": 0, "trace": True}):
         with pytest.raises(ValueError):
             binding.AttentionConfig(**bad_cfg)
+
+
+def test_host_sanitizer_build_leaves_device_code_alone():
+    """The opt-in host-sanitizer target (python -m fa_amd.build --sanitize)
+    puts every -fsanitize= behind -Xarch_host, so no GPU code is built with
+    a sanitizer, and the default builds never include it."""
+    from fa_amd import build
+
+    flags = build.HOSTSAN.flags
+    sanitizers = [i for i, f in enumerate(flags) if f.startswith("-fsanitize")]
+    assert sanitizers and all(flags[i - 1] == "-Xarch_host" for i in sanitizers)
+    assert not any(f.startswith("-fsanitize") for f in build.FLAGS)
+    assert build.HOSTSAN not in build.TARGETS
+    assert build.HOSTSAN.library != build.LIBRARY
+    assert build.identity(build.HOSTSAN) != build.identity(build.ATTENTION)
